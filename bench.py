@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Decode throughput of the Granite-3B-shaped MoE on one MI355X.
+
+Workload: Granite-3.1-3B-a800m shape (32 layers, hidden
+1536, 24/8 heads, 40 experts top-8, intermediate 512, vocab 49155), random
+bf16 weights, batch 64, random prompts of 1024 tokens, 256 new tokens, greedy,
+each decode step replayed as one hipGraph.
+
+A "step" is one decode step of the whole batch (64 tokens). After prefill,
+W untimed steps run and the state is restored; then exactly K steps are timed
+between device synchronisations (K = 255 covers the whole 256-token
+generation, context 1024 -> 1279). ``value`` = 64 * K / elapsed.
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel (expert gate/up GEMM), timed with HIP
+                events on its stream over all 32 layers' weights (no cache
+                reuse across launches), against 8 TB/s;
+  fused_moe     the whole per-layer MoE (align + gate_up + down + combine);
+  cpu_baseline  the CPU oracle (LiteMoE's torch CPU decode path restated) on a
+                bounded sample of the same decode step, extrapolated;
+  engine_decode_tps  the reference's own metric from Engine.generate()
+                (decode_tokens / decode_s with the async output ring).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tok/s, Granite-3B-shape bf16 bs=64; fused-MoE HBM GB/s % of peak"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=255)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--prompt", type=int, default=1024)
+    ap.add_argument("--new-tokens", type=int, default=256)
+    ap.add_argument("--model", default="granite-3b")
+    ap.add_argument("--roofline-reps", type=int, default=10)
+    ap.add_argument("--cpu-layers", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-engine", action="store_true")
+    return ap.parse_args()
+
+
+def moe_roofline(model, cfg, batch, reps):
+    """Time the gate/up kernel and the whole fused MoE per layer with HIP
+    events on the launch stream, rotating over every layer's weights."""
+    import torch
+
+    from litemoe_amd import _lib, experts, router
+    dev = model.w["embedding"].device
+    H, I, E, k = cfg.hidden_size, cfg.intermediate_size, cfg.num_local_experts, cfg.num_experts_per_tok
+    gen = torch.Generator(device=dev).manual_seed(7)
+    z = torch.randn(batch, H, device=dev, generator=gen).to(torch.bfloat16)
+    per_layer = []
+    for w in model.w["layers"]:
+        weights, ids = router.route(z, w["block_sparse_moe.router.layer"], k)
+        offsets, order, _ = experts.moe_align(ids, E)
+        act = torch.empty(batch * k, I, device=dev, dtype=torch.bfloat16)
+        active = int(torch.unique(ids).numel())
+        per_layer.append((w, weights, ids, offsets, order, act, active))
+    stream = _lib.stream(dev)
+    out = torch.empty(batch, H, device=dev, dtype=torch.bfloat16)
+
+    def gate_up_all():
+        for w, weights, ids, offsets, order, act, _ in per_layer:
+            _lib.call("lm_moe_gate_up", z.data_ptr(), w["input_linear"].data_ptr(), offsets.data_ptr(),
+                      order.data_ptr(), batch * k, k, H, I, E, 0, act.data_ptr(), stream)
+
+    def fused_all():
+        for w, weights, ids, *_ in per_layer:
+            experts.fused_experts(z, w["input_linear"], w["output_linear"], weights, ids, out=out)
+
+    result = {}
+    for name, fn in (("gate_up", gate_up_all), ("fused", fused_all)):
+        fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        result[name] = start.elapsed_time(end) * 1e3 / (reps * len(per_layer))  # us per launch
+    active = sum(p[-1] for p in per_layer) / len(per_layer)
+    # Algorithmic bytes (weights of active experts + activations in/out).
+    gate_up_bytes = active * 2 * I * H * 2 + batch * H * 2 + batch * k * I * 2
+    fused_bytes = active * 3 * I * H * 2 + 2 * batch * H * 2 + batch * k * 8
+    return dict(gate_up_us=result["gate_up"], fused_us=result["fused"], active=active,
+                gate_up_bytes=gate_up_bytes, fused_bytes=fused_bytes)
+
+
+def cpu_baseline(model, cfg, engine, state, layers, batch):
+    """Time the CPU oracle's decode step on ``layers`` of the model's layers
+    (weights and filled KV cache copied from the GPU), extrapolate to all."""
+    import torch
+
+    from oracle import granite as oracle
+    torch.set_num_threads(min(16, len(os.sched_getaffinity(0))))
+    cores = torch.get_num_threads()
+
+    def sample(n):
+        sub = cfg.__class__(**{**cfg.to_dict(), "num_hidden_layers": n})
+        w = {"embedding": model.w["embedding"].cpu(), "norm": model.w["norm"].cpu(),
+             "head": model.w["head"].cpu(),
+             "layers": [{k: v.cpu() for k, v in model.w["layers"][i].items()} for i in range(n)]}
+        ref = oracle.Granite(sub, w, engine.capacity, fused=False)
+        cache = oracle.Cache(sub, batch, engine.capacity, torch.bfloat16)
+        if n:
+            cache.k.copy_(engine.cache.k[:n].cpu())
+            cache.v.copy_(engine.cache.v[:n].cpu())
+        tokens, lengths = state["next"].cpu(), state["length"].cpu()
+        valid = torch.ones(batch, dtype=torch.bool)
+        ref.decode(tokens, lengths, valid, cache)  # warm-up
+        times = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            ref.decode(tokens, lengths, valid, cache)
+            times.append(time.perf_counter() - t0)
+        return min(times)
+
+    t0 = sample(0)
+    tl = sample(layers)
+    step = t0 + (tl - t0) * cfg.num_hidden_layers / layers
+    return dict(value=batch / step, unit="tok/s", cores=cores, kind="port",
+                sample=(f"CPU oracle decode step (LiteMoE torch CPU path: per-row bf16 GEMMs, masked attention, "
+                        f"index_add combine) at batch {batch}, context {int(state['length'][0])}, timed on "
+                        f"{layers} of {cfg.num_hidden_layers} layers plus embedding/head ({tl:.2f} s per step) "
+                        f"and extrapolated to {cfg.num_hidden_layers} layers ({step:.1f} s per step)"))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    if not 1 <= args.steps <= args.new_tokens - 1:
+        print("--steps must be in [1, new_tokens - 1]", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from litemoe_amd import synth
+    from litemoe_amd.config import preset
+    from litemoe_amd.engine import Request
+    from litemoe_amd.ep import ExpertParallel
+    from litemoe_amd.experts import HipFusedExperts
+    from litemoe_amd.model import Granite
+    from litemoe_amd.optimized import OptimizedEngine, optimized_policy
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = preset(args.model)
+    t = time.perf_counter()
+    w = synth.granite_weights(cfg, seed=0, device=dev, method="torch")
+    torch.cuda.synchronize()
+    log(f"weights {args.model} generated in {time.perf_counter() - t:.1f}s")
+    ep = ExpertParallel(1, 0, args.batch, cfg.hidden_size, cfg.num_experts_per_tok, torch.bfloat16, dev,
+                        HipFusedExperts())
+    model = Granite(cfg, w, ep, 4096)
+    prompts = synth.prompts(args.batch, args.prompt, cfg.vocab_size, 1)
+    requests = [Request(str(i), p, args.new_tokens) for i, p in enumerate(prompts)]
+    engine = OptimizedEngine(model, requests, mode="graph", ignore_eos=True)
+    with torch.inference_mode():
+        t = time.perf_counter()
+        engine.prepare_graph()
+        torch.cuda.synchronize()
+        log(f"decode step captured in {time.perf_counter() - t:.1f}s (capacity {engine.capacity})")
+        engine.reset()
+        t = time.perf_counter()
+        engine.prefill()
+        torch.cuda.synchronize()
+        log(f"prefill of {args.batch}x{args.prompt} tokens in {time.perf_counter() - t:.2f}s")
+        snapshot = {k: v.clone() for k, v in engine.state.items()}
+        for _ in range(args.warmup):
+            engine.graph.replay()
+        torch.cuda.synchronize()
+        for k, v in snapshot.items():
+            engine.state[k].copy_(v)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            engine.graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        assert bool(engine.state["active"].all() or args.steps == args.new_tokens - 1)
+        log(f"timed {args.steps} decode steps in {elapsed:.3f}s")
+        value = args.batch * args.steps / elapsed
+
+        roof = moe_roofline(model, cfg, args.batch, args.roofline_reps)
+        log(f"gate_up {roof['gate_up_us']:.1f} us/launch, fused MoE {roof['fused_us']:.1f} us/layer")
+
+        engine_tps = None
+        if not args.no_engine:
+            _, metrics = engine.generate()
+            engine_tps = metrics["decode_tps"]
+            log(f"Engine.generate decode_tps {engine_tps:.1f}")
+
+        cpu = None
+        if not args.no_cpu_baseline:
+            for k, v in snapshot.items():
+                engine.state[k].copy_(v)
+            with optimized_policy(engine):
+                engine.prefill()
+            torch.cuda.synchronize()
+            cpu = cpu_baseline(model, cfg, engine, snapshot, args.cpu_layers, args.batch)
+            log(f"cpu baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+
+    gate_gbs = roof["gate_up_bytes"] / (roof["gate_up_us"] * 1e-6) / 1e9
+    fused_gbs = roof["fused_bytes"] / (roof["fused_us"] * 1e-6) / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights N(0,0.02) (torch generator, seed 0), random prompt ids (seed 1)",
+        "config": {"workload": (f"cfg3 decode: {args.model} shape (32 layers, hidden 1536, 24/8 heads, 40 experts "
+                                f"top-8, intermediate 512), batch {args.batch}, prompt {args.prompt}, "
+                                f"{args.new_tokens} new tokens, greedy, one hipGraph per decode step"),
+                   "global_batch": args.batch, "seq_len": args.prompt, "new_tokens": args.new_tokens,
+                   "capacity": engine.capacity, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "gate_up_kernel (lm_moe_gate_up)",
+                     "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": int(roof["gate_up_bytes"]), "us_per_launch": round(roof["gate_up_us"], 2),
+                     "active_experts": roof["active"]},
+        "fused_moe": {"achieved": round(fused_gbs, 1), "unit": "GB/s", "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
+                      "us_per_layer": round(roof["fused_us"], 2), "bytes_per_layer": int(roof["fused_bytes"])},
+        "engine_decode_tps": None if engine_tps is None else round(engine_tps, 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,248 @@
+/*
+ * litemoe_amd — C ABI of the MI355X (gfx950) MoE decode/prefill hot path.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, plain integer sizes and a HIP stream passed as
+ *     `void *` (a hipStream_t; NULL is the legacy default stream);
+ *   - launches its kernels on that stream and returns at once: no allocation,
+ *     no host<->device copy and no synchronisation, so every call can be
+ *     recorded into a HIP graph by stream capture;
+ *   - returns LM_OK (0) or a nonzero status (see lm_status_string).
+ * Scratch memory ("workspace") is supplied by the caller; its size comes from
+ * the matching *_workspace_size query.
+ *
+ * Element types: "bf16" is IEEE bfloat16 stored as uint16, round-to-nearest-
+ * even wherever a float result is stored. Matrices are row-major; strides are
+ * in elements.
+ *
+ * Each declaration names the reference interface it replaces
+ * (ZhuLinsen/LiteMoE, path:line).
+ */
+#ifndef LITEMOE_AMD_H
+#define LITEMOE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LM_OK = 0,
+  LM_EINVAL = 1,        /* invalid argument (null pointer, negative size, bad shape) */
+  LM_EUNSUPPORTED = 2,  /* shape this build has no kernel for (e.g. head_dim != 64) */
+  LM_ELAUNCH = 3,       /* the HIP runtime rejected a kernel launch */
+  LM_EWORKSPACE = 4     /* workspace smaller than the size query returned */
+};
+
+/* Library version string and a message for a status code. */
+const char *lm_version(void);
+const char *lm_status_string(int status);
+
+/* ---------------------------------------------------------------- norms -- */
+
+/* y[r,:] = bf16( bf16(x[r,:] * rsqrt(mean(x[r,:]^2) + eps)) * w ), fp32 math.
+ * Replaces litemoe/norm.py:19-29 (`norm.rmsnorm` -> Triton `_rms`,
+ * norm.py:7-16), which restates model.py:9-11. x, y: [rows, hidden] bf16,
+ * contiguous; w: [hidden] bf16. y may not alias x. */
+int lm_rmsnorm(const void *x, const void *weight, void *y, int64_t rows,
+               int64_t hidden, float eps, void *stream);
+
+/* Residual add fused with the next RMSNorm:
+ *   x[r,:] <- bf16(x[r,:] + alpha * a[r,:]);  y[r,:] = rmsnorm(x[r,:]).
+ * Replaces the pair litemoe/model.py:108-109 (and :122 + :106 of the next
+ * layer): `x.add(a, alpha=residual_multiplier)` then `norm.rmsnorm`. a may be
+ * NULL (then x is only normalised). x is updated in place. */
+int lm_add_rmsnorm(void *x, const void *a, float alpha, const void *weight,
+                   void *y, int64_t rows, int64_t hidden, float eps,
+                   void *stream);
+
+/* ------------------------------------------------------- rope + kv cache -- */
+
+/* Masked KV store, one writer per (row, head, channel):
+ *   if active[r] and 0 <= pos[r] < capacity and 0 <= slot[r] < cache_batch:
+ *     kc[slot[r], h, pos[r], c] = k[r*ks0 + h*ks1 + c*ks3]   (same for v)
+ * Replaces litemoe/kv_write.py:23-29 (Triton `_store`, kv_write.py:6-20;
+ * target index kv_write.py:16). The cache layer is [cache_batch, heads,
+ * capacity, head_dim] contiguous. elem_bytes is 2 (bf16) or 4 (fp32): the
+ * store is a bit copy. positions and slots are int64; slots may be NULL
+ * (identity: slot = row); active is bool (one byte per row). Rows whose
+ * position or slot is out of range are skipped (the reference leaves them
+ * undefined). */
+int lm_kv_write(const void *k, int64_t ks0, int64_t ks1, int64_t ks3,
+                const void *v, int64_t vs0, int64_t vs1, int64_t vs3,
+                void *k_cache, void *v_cache, const int64_t *positions,
+                const uint8_t *active, const int64_t *slots, int64_t rows,
+                int64_t heads, int64_t head_dim, int64_t capacity,
+                int64_t cache_batch, int64_t elem_bytes, void *stream);
+
+/* Neox rotary embedding on q and k fused with the masked KV store.
+ * For every row r (positions[r] indexes cos_sin, [table_len, head_dim] bf16
+ * holding cat(cos[:, :D/2], sin[:, :D/2]) as built at litemoe/model.py:31-35):
+ *   q[r,h,i]     <- x1*cos - x2*sin,  q[r,h,i+D/2] <- x2*cos + x1*sin
+ * with x1 = q[r,h,i], x2 = q[r,h,i+D/2], i < D/2 (fp32 math, one rounding),
+ * and the same rotation of k, which is stored into k_cache at
+ * (slot[r], h, pos[r]) under the lm_kv_write mask, v stored unrotated.
+ * write_k (nonzero) also writes rotated k back in place (prefill needs it).
+ * Replaces vLLM `_custom_ops.rotary_embedding(positions, q, k, D, cos_sin,
+ * is_neox=True)` at litemoe/model.py:58,63-64 followed by `cache.write`
+ * (model.py:59,70 -> kv_write.py:23-29). q, k, v rows have a row stride and a
+ * head stride; channels are contiguous. head_dim must be 64. With k_cache and
+ * v_cache both NULL nothing is stored (v and active may then be NULL): the
+ * call is vLLM's in-place rotary_embedding alone. */
+int lm_rope_kv_write(void *q, int64_t qs0, int64_t qs1, void *k, int64_t ks0,
+                     int64_t ks1, const void *v, int64_t vs0, int64_t vs1,
+                     const void *cos_sin, int64_t table_len,
+                     const int64_t *positions, const uint8_t *active,
+                     const int64_t *slots, void *k_cache, void *v_cache,
+                     int64_t rows, int64_t q_heads, int64_t kv_heads,
+                     int64_t head_dim, int64_t capacity, int64_t cache_batch,
+                     int write_k, void *stream);
+
+/* ------------------------------------------------------------ attention -- */
+
+/* Workspace for lm_flash_decode with the given split count. */
+int lm_flash_decode_workspace_size(int64_t batch, int64_t q_heads,
+                                   int64_t head_dim, int64_t num_splits,
+                                   int64_t *bytes);
+
+/* Split-K decode attention over each row's contiguous KV sequence:
+ *   out[b,h,:] = softmax(scale * q[b,h,:] . K[b,h/G,j,:], j < used[b]) V
+ * K/V layer caches are [batch, kv_heads, capacity, head_dim] bf16 (row b is
+ * cache page b), G = q_heads / kv_heads. used[b] (int32) is clamped to
+ * [0, max_len] and to capacity; a row with used 0 gives zeros. The key range
+ * [0, max_len) is cut into num_splits chunks, combined by log-sum-exp.
+ * Replaces litemoe/flash_decode.py:16-34 (`FlashDecode.__call__` ->
+ * vLLM `flash_attn_varlen_func(..., seqused_k, block_table=arange(B),
+ * num_splits=0)`, flash_decode.py:19-22; aten varlen FA, :30-34). q: row
+ * stride qs0, head stride qs1, channels contiguous; out: [batch, q_heads,
+ * head_dim] contiguous bf16. head_dim must be 64. */
+int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1,
+                    const void *k_cache, const void *v_cache,
+                    const int32_t *used, int64_t batch, int64_t q_heads,
+                    int64_t kv_heads, int64_t capacity, int64_t head_dim,
+                    float scale, int64_t max_len, int64_t num_splits, void *out,
+                    void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Variable-length attention over a packed batch (one row per token):
+ * sequence s owns tokens [cu[s], cu[s+1]); token i of it attends keys
+ * [0, i] of the same sequence when causal, all of them otherwise.
+ * Replaces litemoe/packed.py:12-16 (`PackedPrefill.attention` ->
+ * `aten._flash_attention_forward(q, k, v, cu, cu, max, max, 0.0, causal=True,
+ * False, scale)`). q: [tokens, q_heads, 64], k/v: [tokens, kv_heads, 64] with
+ * row/head strides, channels contiguous; out: [tokens, q_heads, 64]
+ * contiguous bf16; cu: int32 [num_seqs + 1]; max_len bounds every sequence. */
+int lm_prefill_attention(const void *q, int64_t qs0, int64_t qs1,
+                         const void *k, int64_t ks0, int64_t ks1,
+                         const void *v, int64_t vs0, int64_t vs1,
+                         const int32_t *cu_seqlens, int64_t num_seqs,
+                         int64_t tokens, int64_t max_len, int64_t q_heads,
+                         int64_t kv_heads, int64_t head_dim, float scale,
+                         int causal, void *out, void *stream);
+
+/* --------------------------------------------------------------- router -- */
+
+/* Fused router: logits = bf16(x . Wr^T) (fp32 accumulation), then top-k with
+ * ties to the lower expert id, then weights:
+ *   renormalize != 0: softmax over the k selected logits (fp32);
+ *   renormalize == 0: softmax over all E logits, taken at the k selected.
+ * ids come out in descending logit order. logits_out (bf16 [tokens, experts])
+ * may be NULL. Replaces the router GEMV `linear_rows(z, router.layer)`
+ * (litemoe/model.py:110, ops.py:7-12) and vLLM `fused_topk(z, scores, k,
+ * renormalize=True)` (model.py:111-113); on the CPU path `topk` + softmax
+ * (model.py:115-116). x: [tokens, hidden] bf16, Wr: [experts, hidden] bf16,
+ * hidden % 8 == 0, experts <= 256, topk <= min(experts, 16). */
+int lm_router(const void *x, const void *gate_weight, int64_t tokens,
+              int64_t hidden, int64_t experts, int64_t topk, int renormalize,
+              void *logits_out, float *topk_weights, int32_t *topk_ids,
+              void *stream);
+
+/* Selection alone, from given bf16 logits [tokens, experts]; same rules as
+ * lm_router. Replaces vLLM `fused_topk` (litemoe/model.py:112-113) given
+ * `scores`. */
+int lm_topk_softmax(const void *logits, int64_t tokens, int64_t experts,
+                    int64_t topk, int renormalize, float *topk_weights,
+                    int32_t *topk_ids, void *stream);
+
+/* Deterministic stable permutation of routes r = t*topk + j by local expert
+ * id: key = ids[r] - first_expert when in [0, local_experts), else
+ * local_experts (the ignored tail). Writes expert_offsets [local_experts + 1]
+ * (exclusive prefix of the counts; entry local_experts = number of local
+ * routes), sorted_routes [routes] (route ids in key order, ascending route id
+ * within a key: argsort(key, stable=True)) and, if not NULL, inverse [routes]
+ * (inverse[sorted_routes[p]] = p). Replaces the dispatch bookkeeping of
+ * litemoe/ops.py:163-173 (`Grouped.__call__`: local ids, argsort, counts,
+ * offsets) and ops.py:34-40 (`reference_experts`). local_experts <= 511. */
+int lm_moe_align(const int32_t *ids, int64_t routes, int64_t first_expert,
+                 int64_t local_experts, int32_t *expert_offsets,
+                 int32_t *sorted_routes, int32_t *inverse, void *stream);
+
+/* -------------------------------------------------------------- experts -- */
+
+/* Workspace for lm_fused_experts. */
+int lm_fused_experts_workspace_size(int64_t tokens, int64_t topk,
+                                    int64_t hidden, int64_t inter,
+                                    int64_t experts, int64_t *bytes);
+
+/* SwiGLU mixture of experts with the weighted combine:
+ *   out[t] = sum_j w[t,j] * W2[e] . (silu(W13[e,:I] . x[t]) * (W13[e,I:] . x[t])),
+ *   e = ids[t,j].
+ * Rounding follows the reference CPU path: gate/up rounded to bf16, silu
+ * rounded, product rounded, each route's W2 output rounded, then the fp32
+ * ordered combine of lm_moe_finish (routes of a token summed in ascending
+ * (expert id, branch) order, each term bf16(bf16(y) * bf16(w))).
+ * Replaces vLLM `fused_experts(x, w1, w2, topk_weights, topk_ids,
+ * apply_router_weight_on_input=False, global_num_experts=E)` as called at
+ * litemoe/ep.py:40-41 and vllm_moe.py:25-26. x: [tokens, hidden] bf16,
+ * w13: [experts, 2*inter, hidden] bf16 (gate rows first, ops.py:45),
+ * w2: [experts, hidden, inter] bf16, topk_weights fp32 [tokens, topk],
+ * topk_ids int32 [tokens, topk], out: [tokens, hidden] bf16.
+ * hidden % 128 == 0, inter % 128 == 0, hidden / 128 and inter / 128 in
+ * {1, 2, 3, 4, 6, 8, 12, 16}. block_rows (0 = automatic) is the number of
+ * routes one workgroup carries per weight tile (a multiple of 16). logical
+ * (int64 [experts] or NULL for identity) only reorders the combine, as in
+ * lm_moe_finish. */
+int lm_fused_experts(const void *x, const void *w13, const void *w2,
+                     const float *topk_weights, const int32_t *topk_ids,
+                     const int64_t *logical, int64_t tokens, int64_t hidden,
+                     int64_t inter, int64_t experts, int64_t topk,
+                     int64_t block_rows, void *out, void *workspace,
+                     int64_t workspace_bytes, void *stream);
+
+/* Stage entry points of lm_fused_experts, exposed for parity tests.
+ * gate_up: act[p, :] = bf16(silu(bf16(g)) * bf16(u)) for sorted position p,
+ *   g/u = W13[e] . x[sorted_routes[p] / topk]; act is [routes, inter].
+ * down: y[sorted_routes[p], :] = bf16(W2[e] . act[p, :]); y is [routes,
+ *   hidden] in route order. Routes of the ignored tail are not touched. */
+int lm_moe_gate_up(const void *x, const void *w13,
+                   const int32_t *expert_offsets, const int32_t *sorted_routes,
+                   int64_t routes, int64_t topk, int64_t hidden, int64_t inter,
+                   int64_t experts, int64_t block_rows, void *act,
+                   void *stream);
+int lm_moe_down(const void *act, const void *w2, const int32_t *expert_offsets,
+                const int32_t *sorted_routes, int64_t routes, int64_t hidden,
+                int64_t inter, int64_t experts, int64_t block_rows, void *y,
+                void *stream);
+
+/* Weighted combine of route outputs, fp32 ordered accumulation:
+ *   out[t,:] = bf16( sum over j in ascending (logical[ids[t,j]]*K + j) of
+ *                    bf16(bf16(y[row]) * bf16(scales[t,j])) ),
+ * row = inverse(order)[t*K + j] when order is given (y in sorted order),
+ * else t*K + j (y in route order). Routes whose expert id is outside
+ * [rank*count, (rank+1)*count) are skipped and their rows never read.
+ * Replaces litemoe/moe_finish.py:34-57 (`finish`, Triton `_finish`
+ * moe_finish.py:7-31). y: [tokens*K, hidden] bf16; ids int32 [tokens, K];
+ * order int64 [tokens*K] or NULL; scales fp32 [tokens, K]; logical int64
+ * [experts] or NULL (identity); out [tokens, hidden] bf16; 1 <= K <= 8.
+ * workspace: 4*tokens*K bytes when order is given, else may be NULL. */
+int lm_moe_finish(const void *y, const int32_t *ids, const int64_t *order,
+                  const float *scales, const int64_t *logical, void *out,
+                  int64_t tokens, int64_t hidden, int64_t topk, int64_t rank,
+                  int64_t count, void *workspace, int64_t workspace_bytes,
+                  void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LITEMOE_AMD_H */

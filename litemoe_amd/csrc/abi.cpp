@@ -1,0 +1,15 @@
+// Version and status strings of the C ABI.
+#include "../../include/litemoe_amd.h"
+
+extern "C" const char *lm_version(void) { return "litemoe_amd 0.1.0 gfx950"; }
+
+extern "C" const char *lm_status_string(int status) {
+  switch (status) {
+    case LM_OK: return "ok";
+    case LM_EINVAL: return "invalid argument";
+    case LM_EUNSUPPORTED: return "unsupported shape";
+    case LM_ELAUNCH: return "kernel launch failed";
+    case LM_EWORKSPACE: return "workspace too small";
+    default: return "unknown status";
+  }
+}

@@ -1,0 +1,277 @@
+// Split-K decode attention over the contiguous per-row KV cache
+// [batch, kv_heads, capacity, 64] (one "page" per row, as the reference's
+// paged call uses block_table = arange(batch), litemoe/flash_decode.py:10-12).
+//
+// Workgroup (split, kv head, row) covers keys [split*chunk, (split+1)*chunk)
+// clipped to used[row]. Lane l owns key slot l/4 of each 16-key group and
+// channels 16*(l%4) .. +15; it keeps its own online-softmax state (max, sum,
+// 16-channel accumulator) for the G query heads of the kv head, so no
+// cross-lane reduction is needed inside the key loop except the 4-lane dot
+// product sum. States are merged by log-sum-exp across lanes, waves, and
+// (second kernel) splits.
+//
+// Reference semantics: softmax(scale * q.K^T) V over keys j < seqused_k,
+// litemoe/flash_decode.py:16-22; masking litemoe/cache.py:42-47.
+#include "internal.h"
+
+namespace lm {
+namespace {
+
+constexpr int kD = 64;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kKeysPerWave = 16;   // 64 lanes / 4 lanes per key
+constexpr int kUnroll = 2;         // key groups in flight per lane
+
+struct Partial {
+  float *o;  // [batch, q_heads, splits, 64]
+  float *m;  // [batch, q_heads, splits]
+  float *l;  // [batch, q_heads, splits]
+};
+
+__device__ __forceinline__ float merge_factor(float m, float mnew) {
+  return m == -INFINITY ? 0.f : __expf(m - mnew);
+}
+
+template <int G>
+__global__ void __launch_bounds__(kThreads)
+decode_partial_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1,
+                      const bf16 *__restrict__ kc, const bf16 *__restrict__ vc,
+                      const int32_t *__restrict__ used, int q_heads, int kv_heads,
+                      int64_t capacity, float scale, int max_len, int chunk, int splits,
+                      Partial part, bf16 *__restrict__ out) {
+  __shared__ float sm_o[kWaves][G][kD];
+  __shared__ float sm_m[kWaves][G];
+  __shared__ float sm_l[kWaves][G];
+  const int split = blockIdx.x, h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  int n = used[b];
+  n = min(n, max_len);
+  n = (int)min((int64_t)n, capacity);
+  const int k0 = split * chunk;
+  const int k1 = min(n, k0 + chunk);
+  if (splits > 1 && k0 >= n) return;  // the combine kernel skips empty splits
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int ks = lane / 4, dc = lane % 4;
+  // q channels 16*dc .. +15 of the G heads, pre-scaled.
+  float qv[G][16];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const bf16 *qp = q + b * qs0 + (int64_t)(h * G + g) * qs1 + dc * 16;
+    float f[8];
+    unpack8(*reinterpret_cast<const u32x4 *>(qp), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qv[g][i] = f[i] * scale;
+    unpack8(*reinterpret_cast<const u32x4 *>(qp + 8), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qv[g][8 + i] = f[i] * scale;
+  }
+  float m[G], l[G], acc[G][16];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[g][i] = 0.f;
+  }
+  const int64_t head_base = ((int64_t)b * kv_heads + h) * capacity * kD + dc * 16;
+  const bf16 *kbase = kc + head_base;
+  const bf16 *vbase = vc + head_base;
+  constexpr int kStep = kWaves * kKeysPerWave * kUnroll;
+  for (int j0 = k0 + wave * kKeysPerWave * kUnroll; j0 < k1; j0 += kStep) {
+    u32x4 kw[kUnroll][2], vw[kUnroll][2];
+    bool ok[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int j = j0 + u * kKeysPerWave + ks;
+      ok[u] = j < k1;
+      const int64_t off = (int64_t)(ok[u] ? j : k0) * kD;
+      kw[u][0] = *reinterpret_cast<const u32x4 *>(kbase + off);
+      kw[u][1] = *reinterpret_cast<const u32x4 *>(kbase + off + 8);
+      vw[u][0] = *reinterpret_cast<const u32x4 *>(vbase + off);
+      vw[u][1] = *reinterpret_cast<const u32x4 *>(vbase + off + 8);
+    }
+    float s[kUnroll][G];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float kf[16];
+      unpack8(kw[u][0], kf);
+      unpack8(kw[u][1], kf + 8);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d = fmaf(qv[g][i], kf[i], d);
+        d += shfl_xor(d, 1);
+        d += shfl_xor(d, 2);
+        s[u][g] = ok[u] ? d : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = m[g];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) mx = fmaxf(mx, s[u][g]);
+      if (mx == -INFINITY) continue;
+      const float corr = merge_factor(m[g], mx);
+      m[g] = mx;
+      l[g] *= corr;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[g][i] *= corr;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const float p = __expf(s[u][g] - mx);
+        l[g] += p;
+        float vf[16];
+        unpack8(vw[u][0], vf);
+        unpack8(vw[u][1], vf + 8);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
+      }
+    }
+  }
+  // Merge the 16 key slots of the wave (lanes with equal dc).
+#pragma unroll
+  for (int mask = 4; mask < kWave; mask <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mo = shfl_xor(m[g], mask);
+      const float lo = shfl_xor(l[g], mask);
+      const float mn = fmaxf(m[g], mo);
+      const float fa = merge_factor(m[g], mn), fb = merge_factor(mo, mn);
+      l[g] = l[g] * fa + lo * fb;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[g][i] = acc[g][i] * fa + shfl_xor(acc[g][i], mask) * fb;
+      m[g] = mn;
+    }
+  }
+  if (ks == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sm_o[wave][g][dc * 16 + i] = acc[g][i];
+      if (dc == 0) {
+        sm_m[wave][g] = m[g];
+        sm_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  // Threads (g, channel) merge the waves.
+  for (int t = threadIdx.x; t < G * kD; t += kThreads) {
+    const int g = t / kD, c = t % kD;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w][g]);
+    float lsum = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = merge_factor(sm_m[w][g], mx);
+      lsum += sm_l[w][g] * f;
+      o += sm_o[w][g][c] * f;
+    }
+    const int hq = h * G + g;
+    if (splits == 1) {
+      out[((int64_t)b * q_heads + hq) * kD + c] = (bf16)f32_to_bf16(lsum > 0.f ? o / lsum : 0.f);
+    } else {
+      const int64_t slot = ((int64_t)b * q_heads + hq) * splits + split;
+      part.o[slot * kD + c] = o;
+      if (c == 0) {
+        part.m[slot] = mx;
+        part.l[slot] = lsum;
+      }
+    }
+  }
+}
+
+// grid (q_heads, batch), one thread per channel.
+__global__ void __launch_bounds__(kD)
+decode_combine_kernel(const int32_t *__restrict__ used, int q_heads, int64_t capacity, int max_len,
+                      int chunk, int splits, Partial part, bf16 *__restrict__ out) {
+  const int hq = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int c = threadIdx.x;
+  int n = used[b];
+  n = min(n, max_len);
+  n = (int)min((int64_t)n, capacity);
+  const int valid = n > 0 ? min(splits, (n + chunk - 1) / chunk) : 0;
+  const int64_t base = ((int64_t)b * q_heads + hq) * splits;
+  float mx = -INFINITY;
+  for (int s = 0; s < valid; ++s) mx = fmaxf(mx, part.m[base + s]);
+  float lsum = 0.f, o = 0.f;
+  for (int s = 0; s < valid; ++s) {
+    const float f = merge_factor(part.m[base + s], mx);
+    lsum += part.l[base + s] * f;
+    o += part.o[(base + s) * kD + c] * f;
+  }
+  out[((int64_t)b * q_heads + hq) * kD + c] = (bf16)f32_to_bf16(lsum > 0.f ? o / lsum : 0.f);
+}
+
+int64_t workspace_bytes(int64_t batch, int64_t q_heads, int64_t splits) {
+  if (splits <= 1) return 0;
+  const int64_t n = batch * q_heads * splits;
+  return n * kD * 4 + 2 * ((n * 4 + 255) / 256 * 256);
+}
+
+}  // namespace
+}  // namespace lm
+
+using namespace lm;
+
+extern "C" int lm_flash_decode_workspace_size(int64_t batch, int64_t q_heads, int64_t head_dim,
+                                              int64_t num_splits, int64_t *bytes) {
+  LM_REQUIRE(bytes && batch >= 0 && q_heads > 0 && num_splits > 0);
+  if (head_dim != kD) return LM_EUNSUPPORTED;
+  *bytes = workspace_bytes(batch, q_heads, num_splits);
+  return LM_OK;
+}
+
+extern "C" int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1, const void *k_cache,
+                               const void *v_cache, const int32_t *used, int64_t batch,
+                               int64_t q_heads, int64_t kv_heads, int64_t capacity,
+                               int64_t head_dim, float scale, int64_t max_len, int64_t num_splits,
+                               void *out, void *workspace, int64_t workspace_bytes_, void *stream) {
+  LM_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 &&
+             capacity > 0 && max_len > 0 && num_splits > 0 && num_splits <= 1024 &&
+             max_len < ((int64_t)1 << 30));
+  if (head_dim != kD) return LM_EUNSUPPORTED;
+  if (batch == 0) return LM_OK;
+  LM_REQUIRE(q && k_cache && v_cache && used && out);
+  const int64_t need = workspace_bytes(batch, q_heads, num_splits);
+  if (need > 0 && (!workspace || workspace_bytes_ < need)) return LM_EWORKSPACE;
+  const int chunk = (int)align_up(cdiv(max_len, num_splits), 16);
+  const int splits = (int)cdiv(max_len, chunk);
+  Partial part{nullptr, nullptr, nullptr};
+  if (splits > 1) {
+    const int64_t n = batch * q_heads * num_splits;
+    char *p = static_cast<char *>(workspace);
+    part.o = reinterpret_cast<float *>(p);
+    part.m = reinterpret_cast<float *>(p + n * kD * 4);
+    part.l = reinterpret_cast<float *>(p + n * kD * 4 + (n * 4 + 255) / 256 * 256);
+  }
+  // Partials are indexed with the caller's split count as the stride.
+  const int stride_splits = splits > 1 ? (int)num_splits : 1;
+  const dim3 grid((unsigned)splits, (unsigned)kv_heads, (unsigned)batch);
+  hipStream_t s = (hipStream_t)stream;
+  const int G = (int)(q_heads / kv_heads);
+  switch (G) {
+#define X(GG)                                                                                    \
+  case GG:                                                                                       \
+    decode_partial_kernel<GG><<<grid, kThreads, 0, s>>>(                                         \
+        (const bf16 *)q, qs0, qs1, (const bf16 *)k_cache, (const bf16 *)v_cache, used,           \
+        (int)q_heads, (int)kv_heads, capacity, scale, (int)max_len, chunk, stride_splits, part,  \
+        (bf16 *)out);                                                                            \
+    break;
+    X(1) X(2) X(3) X(4) X(6) X(8)
+#undef X
+    default:
+      return LM_EUNSUPPORTED;
+  }
+  LM_CHECK_LAUNCH();
+  if (splits > 1) {
+    decode_combine_kernel<<<dim3((unsigned)q_heads, (unsigned)batch), kD, 0, s>>>(
+        used, (int)q_heads, capacity, (int)max_len, chunk, stride_splits, part, (bf16 *)out);
+    LM_CHECK_LAUNCH();
+  }
+  return LM_OK;
+}

@@ -1,0 +1,90 @@
+// Shared device helpers for the gfx950 kernels: bf16 conversion, vector types,
+// wavefront reductions and the launch-status plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/litemoe_amd.h"
+
+namespace lm {
+
+typedef uint16_t bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+// Low / high halves of a packed pair of bf16 values.
+__device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even float -> bf16, NaN -> canonical quiet NaN 0x7fc0
+// (the conversion torch performs).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+// Eight bf16 (one 16-byte word) to floats.
+__device__ __forceinline__ void unpack8(const u32x4 &w, float *f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = lo_f32(w[i]);
+    f[2 * i + 1] = hi_f32(w[i]);
+  }
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 &w) {
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+  return v;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// MFMA 16x16x32 bf16 (gfx950). Lane l supplies row l%16 of A and column l%16
+// of B, each with the eight k values of k-group l/16; it receives C rows
+// 4*(l/16) .. +3 of column l%16.
+__device__ __forceinline__ f32x4 mfma16x16x32(const u32x4 &a, const u32x4 &b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+__host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace lm
+
+// Launch-status check for the C ABI wrappers.
+#define LM_CHECK_LAUNCH()                                      \
+  do {                                                         \
+    if (hipGetLastError() != hipSuccess) return LM_ELAUNCH;    \
+  } while (0)
+
+#define LM_REQUIRE(cond)               \
+  do {                                 \
+    if (!(cond)) return LM_EINVAL;     \
+  } while (0)

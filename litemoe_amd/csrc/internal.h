@@ -1,0 +1,27 @@
+// Launchers shared between translation units of the library (not exported).
+#pragma once
+
+#include "common.h"
+
+namespace lm {
+
+// moe_finish.hip: combine of route outputs (see lm_moe_finish).
+// inverse: sorted position of each route, or nullptr when y is in route order.
+int launch_finish(const bf16 *y, const int32_t *ids, const int32_t *inverse, const float *scales,
+                  const int64_t *logical, bf16 *out, int64_t tokens, int64_t hidden, int64_t topk,
+                  int64_t rank, int64_t count, hipStream_t stream);
+
+// moe_gemm.hip
+int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const int32_t *sorted,
+                   int64_t routes, int64_t topk, int64_t hidden, int64_t inter, int64_t experts,
+                   int64_t block_rows, bf16 *act, hipStream_t stream);
+int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const int32_t *sorted,
+                int64_t routes, int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
+                bf16 *y, hipStream_t stream);
+
+// Rows of one weight-tile block; 0 picks min(align16(tokens), 256).
+int pick_block_rows(int64_t block_rows, int64_t tokens);
+
+inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace lm

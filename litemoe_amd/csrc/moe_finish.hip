@@ -1,0 +1,125 @@
+// Weighted combine of route outputs (the moe_finish contract):
+//   out[t] = bf16( sum_{j in ascending logical(ids[t,j])*K + j}
+//                  bf16(bf16(y[row(t,j)]) * bf16(scales[t,j])) )   (fp32 sum)
+// Non-owned routes are skipped and their rows never read.
+// Reference: litemoe/moe_finish.py:7-31 (`_finish`), :34-57 (`finish`).
+#include "internal.h"
+
+namespace lm {
+namespace {
+
+constexpr int kMaxK = 8;
+
+// grid (tokens, column blocks); each thread owns kCols consecutive columns.
+template <int kCols>
+__global__ void __launch_bounds__(256)
+finish_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ ids,
+              const int32_t *__restrict__ inverse, const float *__restrict__ scales,
+              const int64_t *__restrict__ logical, bf16 *__restrict__ out, int hidden, int topk,
+              int64_t rank, int64_t count) {
+  const int64_t t = blockIdx.x;
+  const int c0 = (blockIdx.y * 256 + threadIdx.x) * kCols;
+  if (c0 >= hidden) return;
+  // Rank of each branch under the key logical*K + j (keys are distinct).
+  int64_t key[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j) {
+    if (j < topk) {
+      const int64_t e = ids[t * topk + j];
+      key[j] = (logical ? logical[e] : e) * topk + j;
+    } else {
+      key[j] = INT64_MAX;
+    }
+  }
+  int order[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j) {
+    int r = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxK; ++i) r += key[i] < key[j];
+    order[j] = r;
+  }
+  float total[kCols];
+#pragma unroll
+  for (int c = 0; c < kCols; ++c) total[c] = 0.f;
+  for (int q = 0; q < topk; ++q) {
+    int sel = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) sel += (order[j] == q) ? j : 0;
+    const int64_t r = t * topk + sel;
+    const int64_t e = (int64_t)ids[r] - rank * count;
+    if (e < 0 || e >= count) continue;
+    const int64_t row = inverse ? (int64_t)inverse[r] : r;
+    const float s = round_bf16(scales[r]);
+    const bf16 *yr = y + row * hidden + c0;
+    if constexpr (kCols == 8) {
+      float v[8];
+      unpack8(*reinterpret_cast<const u32x4 *>(yr), v);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) total[c] += round_bf16(v[c] * s);
+    } else {
+      total[0] += round_bf16(bf16_to_f32(yr[0]) * s);
+    }
+  }
+  bf16 *o = out + t * hidden + c0;
+  if constexpr (kCols == 8) {
+    u32x4 w;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[c] = pack_bf16(total[2 * c], total[2 * c + 1]);
+    *reinterpret_cast<u32x4 *>(o) = w;
+  } else {
+    o[0] = (bf16)f32_to_bf16(total[0]);
+  }
+}
+
+__global__ void __launch_bounds__(256)
+invert_kernel(const int64_t *__restrict__ order, int64_t n, int32_t *__restrict__ inverse) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= n) return;
+  const int64_t r = order[p];
+  if (r >= 0 && r < n) inverse[r] = (int32_t)p;
+}
+
+}  // namespace
+
+int launch_finish(const bf16 *y, const int32_t *ids, const int32_t *inverse, const float *scales,
+                  const int64_t *logical, bf16 *out, int64_t tokens, int64_t hidden, int64_t topk,
+                  int64_t rank, int64_t count, hipStream_t stream) {
+  if (tokens == 0) return LM_OK;
+  if (hidden % 8 == 0) {
+    const dim3 grid((unsigned)tokens, (unsigned)cdiv(hidden, 256 * 8));
+    finish_kernel<8><<<grid, 256, 0, stream>>>(y, ids, inverse, scales, logical, out, (int)hidden,
+                                               (int)topk, rank, count);
+  } else {
+    const dim3 grid((unsigned)tokens, (unsigned)cdiv(hidden, 256));
+    finish_kernel<1><<<grid, 256, 0, stream>>>(y, ids, inverse, scales, logical, out, (int)hidden,
+                                               (int)topk, rank, count);
+  }
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+}  // namespace lm
+
+using namespace lm;
+
+extern "C" int lm_moe_finish(const void *y, const int32_t *ids, const int64_t *order,
+                             const float *scales, const int64_t *logical, void *out,
+                             int64_t tokens, int64_t hidden, int64_t topk, int64_t rank,
+                             int64_t count, void *workspace, int64_t workspace_bytes,
+                             void *stream) {
+  LM_REQUIRE(tokens >= 0 && hidden > 0 && topk >= 1 && topk <= kMaxK && count > 0 && rank >= 0);
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(y && ids && scales && out);
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t routes = tokens * topk;
+  int32_t *inverse = nullptr;
+  if (order) {
+    if (!workspace || workspace_bytes < 4 * routes) return LM_EWORKSPACE;
+    inverse = static_cast<int32_t *>(workspace);
+    invert_kernel<<<dim3((unsigned)cdiv(routes, 256)), 256, 0, s>>>(order, routes, inverse);
+    LM_CHECK_LAUNCH();
+  }
+  return launch_finish((const bf16 *)y, ids, inverse, scales, logical, (bf16 *)out, tokens, hidden,
+                       topk, rank, count, s);
+}

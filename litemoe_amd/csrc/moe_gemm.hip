@@ -1,0 +1,328 @@
+// Grouped SwiGLU expert GEMMs on MFMA (v_mfma_f32_16x16x32_bf16) for the
+// decode-sized MoE, where the expert weights are the HBM traffic:
+//
+//   gate_up: act[p] = bf16(silu(bf16(x_t . W13[e, j])) * bf16(x_t . W13[e, I+j]))
+//   down:    y[r]   = bf16(act[p] . W2[e, n])
+//
+// for sorted position p of route r = sorted[p] (token t = r / topk) of expert
+// e. Workgroup (column tile, row block): 4 waves split the reduction dimension
+// K into quarters; each wave loads its slice of the workgroup's weight tile
+// into registers once, then streams the block's routes through it in 16-row
+// MFMA sub-blocks; the quarters are summed through LDS. A block is at most
+// block_rows routes of one expert, so each expert's weights are read once per
+// block (once per call when block_rows >= the route count of any expert).
+// Blocks are enumerated on the device from expert_offsets, so the grid is
+// fixed by the shapes alone (graph capture) and empty experts cost nothing
+// but an early exit.
+//
+// Reference: the expert math of litemoe/ops.py:43-47 (reference_experts) and
+// the vLLM fused_experts call at litemoe/ep.py:40-41.
+#include "internal.h"
+
+namespace lm {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// Block b of the per-expert blocks of block_rows routes.
+__device__ __forceinline__ bool find_block(const int32_t *__restrict__ offsets, int experts, int bm,
+                                           int b, int &e_out, int &r0, int &r1) {
+  int o0 = offsets[0];
+  for (int e = 0; e < experts; ++e) {
+    const int o1 = offsets[e + 1];
+    const int nb = (o1 - o0 + bm - 1) / bm;
+    if (b < nb) {
+      e_out = e;
+      r0 = o0 + b * bm;
+      r1 = min(o1, r0 + bm);
+      return true;
+    }
+    b -= nb;
+    o0 = o1;
+  }
+  return false;
+}
+
+__device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+// KS: 32-wide k steps per wave, hidden = KS * 32 * kWaves.
+template <int KS>
+__global__ void __launch_bounds__(kThreads)
+gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
+               const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted, int topk,
+               int hidden, int inter, int experts, int bm, bf16 *__restrict__ act) {
+  __shared__ float red[kWaves][2][4][kWave];
+  int e, r0, r1;
+  if (!find_block(offsets, experts, bm, blockIdx.y, e, r0, r1)) return;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int col = lane % 16, grp = lane / 16;
+  const int n0 = blockIdx.x * 16;
+  const int kbase = wave * KS * 32 + grp * 8;
+  const bf16 *wg = w13 + ((int64_t)e * 2 * inter + n0 + col) * hidden + kbase;
+  const bf16 *wu = wg + (int64_t)inter * hidden;
+  u32x4 bg[KS], bu[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    bg[s] = load16(wg + s * 32);
+    bu[s] = load16(wu + s * 32);
+  }
+  for (int rb = r0; rb < r1; rb += 16) {
+    const int p = rb + col;
+    u32x4 a[KS];
+    if (p < r1) {
+      const bf16 *xr = x + (int64_t)(sorted[p] / topk) * hidden + kbase;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) a[s] = load16(xr + s * 32);
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) a[s] = u32x4{0u, 0u, 0u, 0u};
+    }
+    f32x4 cg = {0.f, 0.f, 0.f, 0.f}, cu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      cg = mfma16x16x32(a[s], bg[s], cg);
+      cu = mfma16x16x32(a[s], bu[s], cu);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[wave][0][i][lane] = cg[i];
+      red[wave][1][i][lane] = cu[i];
+    }
+    __syncthreads();
+    // Wave w finishes C row 4*grp + w of every lane group.
+    float g = 0.f, u = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      g += red[w][0][wave][lane];
+      u += red[w][1][wave][lane];
+    }
+    const int row = rb + grp * 4 + wave;
+    if (row < r1) {
+      const float h = round_bf16(silu(round_bf16(g))) * round_bf16(u);
+      act[(int64_t)row * inter + n0 + col] = (bf16)f32_to_bf16(h);
+    }
+    __syncthreads();
+  }
+}
+
+// KS: 32-wide k steps per wave, inter = KS * 32 * kWaves. Column tile of 32
+// (two MFMA tiles).
+template <int KS>
+__global__ void __launch_bounds__(kThreads)
+down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
+            const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted, int hidden,
+            int inter, int experts, int bm, bf16 *__restrict__ y) {
+  __shared__ float red[kWaves][2][4][kWave];
+  int e, r0, r1;
+  if (!find_block(offsets, experts, bm, blockIdx.y, e, r0, r1)) return;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int col = lane % 16, grp = lane / 16;
+  const int n0 = blockIdx.x * 32;
+  const int kbase = wave * KS * 32 + grp * 8;
+  const bf16 *w0 = w2 + ((int64_t)e * hidden + n0 + col) * inter + kbase;
+  const bf16 *w1 = w0 + (int64_t)16 * inter;
+  u32x4 b0[KS], b1[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    b0[s] = load16(w0 + s * 32);
+    b1[s] = load16(w1 + s * 32);
+  }
+  for (int rb = r0; rb < r1; rb += 16) {
+    const int p = rb + col;
+    u32x4 a[KS];
+    if (p < r1) {
+      const bf16 *ar = act + (int64_t)p * inter + kbase;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) a[s] = load16(ar + s * 32);
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) a[s] = u32x4{0u, 0u, 0u, 0u};
+    }
+    f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      c0 = mfma16x16x32(a[s], b0[s], c0);
+      c1 = mfma16x16x32(a[s], b1[s], c1);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[wave][0][i][lane] = c0[i];
+      red[wave][1][i][lane] = c1[i];
+    }
+    __syncthreads();
+    float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      v0 += red[w][0][wave][lane];
+      v1 += red[w][1][wave][lane];
+    }
+    const int row = rb + grp * 4 + wave;
+    if (row < r1) {
+      bf16 *yr = y + (int64_t)sorted[row] * hidden + n0 + col;
+      yr[0] = (bf16)f32_to_bf16(v0);
+      yr[16] = (bf16)f32_to_bf16(v1);
+    }
+    __syncthreads();
+  }
+}
+
+// Supported k steps per wave (reduction length / 128).
+#define LM_KS_LIST(X) X(1) X(2) X(3) X(4) X(6) X(8) X(12) X(16)
+
+}  // namespace
+
+int pick_block_rows(int64_t block_rows, int64_t tokens) {
+  if (block_rows > 0) return (int)block_rows;
+  // Every token picks an expert at most once, so a block of >= tokens rows
+  // holds a whole expert; larger batches trade weight re-reads for blocks.
+  const int64_t bm = align_up(tokens, 16);
+  return (int)(bm > 256 ? 256 : (bm < 16 ? 16 : bm));
+}
+
+int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const int32_t *sorted,
+                   int64_t routes, int64_t topk, int64_t hidden, int64_t inter, int64_t experts,
+                   int64_t block_rows, bf16 *act, hipStream_t stream) {
+  if (routes == 0) return LM_OK;
+  const int bm = (int)block_rows;
+  if (cdiv(routes, bm) + experts > 65535) return LM_EUNSUPPORTED;
+  const dim3 grid((unsigned)(inter / 16), (unsigned)(cdiv(routes, bm) + experts));
+  switch (hidden / 128) {
+#define X(KS)                                                                                 \
+  case KS:                                                                                    \
+    gate_up_kernel<KS><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, (int)topk,     \
+                                                       (int)hidden, (int)inter, (int)experts, \
+                                                       bm, act);                              \
+    break;
+    LM_KS_LIST(X)
+#undef X
+    default:
+      return LM_EUNSUPPORTED;
+  }
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const int32_t *sorted,
+                int64_t routes, int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
+                bf16 *y, hipStream_t stream) {
+  if (routes == 0) return LM_OK;
+  const int bm = (int)block_rows;
+  if (cdiv(routes, bm) + experts > 65535) return LM_EUNSUPPORTED;
+  const dim3 grid((unsigned)(hidden / 32), (unsigned)(cdiv(routes, bm) + experts));
+  switch (inter / 128) {
+#define X(KS)                                                                              \
+  case KS:                                                                                 \
+    down_kernel<KS><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, (int)hidden,  \
+                                                    (int)inter, (int)experts, bm, y);      \
+    break;
+    LM_KS_LIST(X)
+#undef X
+    default:
+      return LM_EUNSUPPORTED;
+  }
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+}  // namespace lm
+
+using namespace lm;
+
+namespace {
+bool expert_shapes_ok(int64_t hidden, int64_t inter) {
+  auto ks_ok = [](int64_t n) {
+    if (n % 128) return false;
+    switch (n / 128) {
+      case 1: case 2: case 3: case 4: case 6: case 8: case 12: case 16: return true;
+      default: return false;
+    }
+  };
+  return ks_ok(hidden) && ks_ok(inter);
+}
+
+struct ExpertWorkspace {
+  int32_t *offsets, *sorted;
+  bf16 *act, *y;
+  int64_t bytes;
+};
+
+ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, int64_t inter,
+                      int64_t experts) {
+  const int64_t routes = tokens * topk;
+  char *p = static_cast<char *>(base);
+  ExpertWorkspace w;
+  int64_t off = 0;
+  w.offsets = reinterpret_cast<int32_t *>(p + off);
+  off += align_up(4 * (experts + 1), 256);
+  w.sorted = reinterpret_cast<int32_t *>(p + off);
+  off += align_up(4 * routes, 256);
+  w.act = reinterpret_cast<bf16 *>(p + off);
+  off += align_up(2 * routes * inter, 256);
+  w.y = reinterpret_cast<bf16 *>(p + off);
+  off += align_up(2 * routes * hidden, 256);
+  w.bytes = off;
+  return w;
+}
+}  // namespace
+
+extern "C" int lm_fused_experts_workspace_size(int64_t tokens, int64_t topk, int64_t hidden,
+                                               int64_t inter, int64_t experts, int64_t *bytes) {
+  LM_REQUIRE(bytes && tokens >= 0 && topk > 0 && hidden > 0 && inter > 0 && experts > 0);
+  *bytes = carve(nullptr, tokens, topk, hidden, inter, experts).bytes;
+  return LM_OK;
+}
+
+extern "C" int lm_moe_gate_up(const void *x, const void *w13, const int32_t *expert_offsets,
+                              const int32_t *sorted_routes, int64_t routes, int64_t topk,
+                              int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
+                              void *act, void *stream) {
+  LM_REQUIRE(routes >= 0 && topk > 0 && experts > 0 && block_rows >= 0 && block_rows % 16 == 0);
+  if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
+  if (routes == 0) return LM_OK;
+  LM_REQUIRE(x && w13 && expert_offsets && sorted_routes && act);
+  return launch_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets, sorted_routes, routes,
+                        topk, hidden, inter, experts, pick_block_rows(block_rows, routes),
+                        (bf16 *)act, (hipStream_t)stream);
+}
+
+extern "C" int lm_moe_down(const void *act, const void *w2, const int32_t *expert_offsets,
+                           const int32_t *sorted_routes, int64_t routes, int64_t hidden,
+                           int64_t inter, int64_t experts, int64_t block_rows, void *y,
+                           void *stream) {
+  LM_REQUIRE(routes >= 0 && experts > 0 && block_rows >= 0 && block_rows % 16 == 0);
+  if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
+  if (routes == 0) return LM_OK;
+  LM_REQUIRE(act && w2 && expert_offsets && sorted_routes && y);
+  return launch_down((const bf16 *)act, (const bf16 *)w2, expert_offsets, sorted_routes, routes,
+                     hidden, inter, experts, pick_block_rows(block_rows, routes), (bf16 *)y,
+                     (hipStream_t)stream);
+}
+
+extern "C" int lm_fused_experts(const void *x, const void *w13, const void *w2,
+                                const float *topk_weights, const int32_t *topk_ids,
+                                const int64_t *logical, int64_t tokens, int64_t hidden,
+                                int64_t inter, int64_t experts,
+                                int64_t topk, int64_t block_rows, void *out, void *workspace,
+                                int64_t workspace_bytes, void *stream) {
+  LM_REQUIRE(tokens >= 0 && topk > 0 && topk <= 8 && topk <= experts && block_rows >= 0 &&
+             block_rows % 16 == 0);
+  if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(x && w13 && w2 && topk_weights && topk_ids && out && workspace);
+  ExpertWorkspace w = carve(workspace, tokens, topk, hidden, inter, experts);
+  if (workspace_bytes < w.bytes) return LM_EWORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t routes = tokens * topk;
+  const int bm = pick_block_rows(block_rows, tokens);
+  int rc = lm_moe_align(topk_ids, routes, 0, experts, w.offsets, w.sorted, nullptr, stream);
+  if (rc) return rc;
+  rc = launch_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, routes, topk,
+                      hidden, inter, experts, bm, w.act, s);
+  if (rc) return rc;
+  rc = launch_down(w.act, (const bf16 *)w2, w.offsets, w.sorted, routes, hidden, inter, experts,
+                   bm, w.y, s);
+  if (rc) return rc;
+  return launch_finish(w.y, topk_ids, nullptr, topk_weights, logical, (bf16 *)out, tokens, hidden,
+                       topk, 0, experts, s);
+}

@@ -1,0 +1,265 @@
+// Fused router (gate GEMV -> top-k -> softmax) and the deterministic
+// expert-sorted route permutation.
+//
+// Selection rule: ids are the k largest bf16 logits in descending order,
+// equal logits ordered by ascending expert id (a stable descending sort).
+// Weights follow vLLM fused_topk / HF GraniteMoeTopKRouter: softmax over the
+// k selected logits (renormalize) or over all E logits.
+// References: litemoe/model.py:110-118, ops.py:7-12, ops.py:163-173.
+#include "common.h"
+
+namespace lm {
+namespace {
+
+constexpr int kRouterThreads = 256;
+constexpr int kMaxExperts = 256;
+constexpr int kMaxTopk = 16;
+
+// Monotone map float -> uint32 (NaN canonicalised above +inf, as torch.topk
+// orders NaN first), combined with the inverted expert id so that a 64-bit
+// max picks the largest value and, among equals, the lowest id.
+__device__ __forceinline__ uint64_t select_key(float v, int e) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) u = 0x7fc00000u;
+  const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const uint32_t hi = shfl_xor((uint32_t)(v >> 32), m);
+    const uint32_t lo = shfl_xor((uint32_t)v, m);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Executed by one full wave. logit[e] (e < experts) holds bf16-rounded
+// logits as floats. Writes topk weights and ids of one token.
+__device__ void select_topk(const float *logit, int experts, int topk, int renormalize,
+                            float *__restrict__ tw, int32_t *__restrict__ tid) {
+  const int lane = threadIdx.x % kWave;
+  uint64_t cand[kMaxExperts / kWave];
+#pragma unroll
+  for (int c = 0; c < kMaxExperts / kWave; ++c) {
+    const int e = lane + c * kWave;
+    cand[c] = e < experts ? select_key(logit[e], e) : 0ull;
+  }
+  // Lane j keeps the j-th selection; every lane sees the running maximum.
+  float mine = 0.f, m = 0.f;
+  int mine_id = 0;
+  for (int j = 0; j < topk; ++j) {
+    uint64_t best = 0ull;
+#pragma unroll
+    for (int c = 0; c < kMaxExperts / kWave; ++c) best = cand[c] > best ? cand[c] : best;
+    best = wave_max_u64(best);
+    const int e = (int)(0xffffffffu - (uint32_t)best);
+    const float v = logit[e];
+    if (j == 0) m = v;
+    if (lane == j) {
+      mine = v;
+      mine_id = e;
+    }
+#pragma unroll
+    for (int c = 0; c < kMaxExperts / kWave; ++c)
+      if (cand[c] == best) cand[c] = 0ull;
+  }
+  const float ex = lane < topk ? expf(mine - m) : 0.f;
+  float denom;
+  if (renormalize) {
+    denom = wave_sum(ex);
+  } else {
+    float part = 0.f;
+    for (int e = lane; e < experts; e += kWave) part += expf(logit[e] - m);
+    denom = wave_sum(part);
+  }
+  if (lane < topk) {
+    tw[lane] = ex / denom;
+    tid[lane] = mine_id;
+  }
+}
+
+// One workgroup per token; wave w computes logits of experts w, w+4, ...
+__global__ void __launch_bounds__(kRouterThreads)
+router_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ wr, int hidden, int experts,
+              int topk, int renormalize, bf16 *__restrict__ logits_out, float *__restrict__ tw,
+              int32_t *__restrict__ tid) {
+  __shared__ float logit[kMaxExperts];
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int nvec = hidden / 8;
+  const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + row * hidden);
+  for (int e = wave; e < experts; e += kRouterThreads / kWave) {
+    const u32x4 *w = reinterpret_cast<const u32x4 *>(wr + (int64_t)e * hidden);
+    float acc = 0.f;
+    for (int i = lane; i < nvec; i += kWave) {
+      float a[8], b[8];
+      unpack8(xr[i], a);
+      unpack8(w[i], b);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf(a[j], b[j], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) {
+      const uint32_t h = f32_to_bf16(acc);
+      logit[e] = bf16_to_f32(h);
+      if (logits_out) logits_out[row * experts + e] = (bf16)h;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) select_topk(logit, experts, topk, renormalize, tw + row * topk, tid + row * topk);
+}
+
+__global__ void __launch_bounds__(kWave)
+topk_from_logits_kernel(const bf16 *__restrict__ logits, int experts, int topk, int renormalize,
+                        float *__restrict__ tw, int32_t *__restrict__ tid) {
+  __shared__ float logit[kMaxExperts];
+  const int64_t row = blockIdx.x;
+  for (int e = threadIdx.x; e < experts; e += kWave) logit[e] = bf16_to_f32(logits[row * experts + e]);
+  __syncthreads();
+  select_topk(logit, experts, topk, renormalize, tw + row * topk, tid + row * topk);
+}
+
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignWaves = kAlignThreads / kWave;
+constexpr int kMaxAlignExperts = 511;
+
+// Lanes of the wave whose key equals this lane's key (among `valid` lanes),
+// from one ballot per key bit.
+__device__ __forceinline__ uint64_t match_key(int key, bool valid, int nbits) {
+  uint64_t eq = __ballot(valid);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (key >> b) & 1;
+    const uint64_t m = __ballot(valid && bit);
+    eq &= bit ? m : ~m;
+  }
+  return eq;
+}
+
+// Single workgroup. Wave w owns the contiguous route segment
+// [w*seg, (w+1)*seg): pass 1 counts keys per segment, a scan turns the
+// counts into per-(segment, key) bases, pass 2 scatters each route to
+// base + its rank among equal keys earlier in the segment. No atomics: the
+// permutation is the stable argsort of the key.
+__global__ void __launch_bounds__(kAlignThreads)
+align_kernel(const int32_t *__restrict__ ids, int routes, int first, int local,
+             int32_t *__restrict__ offsets, int32_t *__restrict__ sorted,
+             int32_t *__restrict__ inverse) {
+  extern __shared__ int smem[];
+  const int keys = local + 1;
+  int *cnt = smem;                            // [kAlignWaves][keys]
+  int *scan = smem + kAlignWaves * keys;      // [2][1024]
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  for (int i = threadIdx.x; i < kAlignWaves * keys; i += kAlignThreads) cnt[i] = 0;
+  __syncthreads();
+  const int seg = (int)(cdiv(cdiv(routes, kAlignWaves), kWave) * kWave);
+  const int begin = wave * seg;
+  const int end = min(routes, begin + seg);
+  const int nbits = 32 - __clz(local);
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int base = begin; base < end; base += kWave) {
+    const int r = base + lane;
+    const bool valid = r < end;
+    int key = local;
+    if (valid) {
+      const int e = ids[r] - first;
+      key = (e >= 0 && e < local) ? e : local;
+    }
+    const uint64_t eq = match_key(key, valid, nbits);
+    if (valid && (eq & below) == 0ull) cnt[wave * keys + key] += __popcll(eq);
+  }
+  __syncthreads();
+  // Totals per key, then an inclusive Hillis-Steele scan over keys.
+  int total = 0;
+  if (threadIdx.x < keys)
+    for (int w = 0; w < kAlignWaves; ++w) total += cnt[w * keys + threadIdx.x];
+  scan[threadIdx.x] = threadIdx.x < keys ? total : 0;
+  __syncthreads();
+  int src = 0;
+  for (int d = 1; d < kAlignThreads; d <<= 1) {
+    const int v = scan[src * kAlignThreads + threadIdx.x] +
+                  (threadIdx.x >= d ? scan[src * kAlignThreads + threadIdx.x - d] : 0);
+    scan[(1 - src) * kAlignThreads + threadIdx.x] = v;
+    src = 1 - src;
+    __syncthreads();
+  }
+  if (threadIdx.x < keys) {
+    int running = scan[src * kAlignThreads + threadIdx.x] - total;  // exclusive
+    offsets[threadIdx.x] = running;
+    for (int w = 0; w < kAlignWaves; ++w) {
+      const int c = cnt[w * keys + threadIdx.x];
+      cnt[w * keys + threadIdx.x] = running;
+      running += c;
+    }
+  }
+  __syncthreads();
+  for (int base = begin; base < end; base += kWave) {
+    const int r = base + lane;
+    const bool valid = r < end;
+    int key = local;
+    if (valid) {
+      const int e = ids[r] - first;
+      key = (e >= 0 && e < local) ? e : local;
+    }
+    const uint64_t eq = match_key(key, valid, nbits);
+    const int rank = __popcll(eq & below);
+    int pos = 0;
+    if (valid) pos = cnt[wave * keys + key] + rank;
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      sorted[pos] = r;
+      if (inverse) inverse[r] = pos;
+      if (rank == 0) cnt[wave * keys + key] += __popcll(eq);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+}  // namespace
+}  // namespace lm
+
+using namespace lm;
+
+extern "C" int lm_router(const void *x, const void *gate_weight, int64_t tokens, int64_t hidden,
+                         int64_t experts, int64_t topk, int renormalize, void *logits_out,
+                         float *topk_weights, int32_t *topk_ids, void *stream) {
+  LM_REQUIRE(tokens >= 0 && hidden > 0 && experts > 0 && topk > 0);
+  if (hidden % 8 || experts > kMaxExperts || topk > kMaxTopk || topk > experts)
+    return LM_EUNSUPPORTED;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(x && gate_weight && topk_weights && topk_ids);
+  router_kernel<<<dim3((unsigned)tokens), kRouterThreads, 0, (hipStream_t)stream>>>(
+      (const bf16 *)x, (const bf16 *)gate_weight, (int)hidden, (int)experts, (int)topk,
+      renormalize, (bf16 *)logits_out, topk_weights, topk_ids);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+extern "C" int lm_topk_softmax(const void *logits, int64_t tokens, int64_t experts, int64_t topk,
+                               int renormalize, float *topk_weights, int32_t *topk_ids,
+                               void *stream) {
+  LM_REQUIRE(tokens >= 0 && experts > 0 && topk > 0);
+  if (experts > kMaxExperts || topk > kMaxTopk || topk > experts) return LM_EUNSUPPORTED;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(logits && topk_weights && topk_ids);
+  topk_from_logits_kernel<<<dim3((unsigned)tokens), kWave, 0, (hipStream_t)stream>>>(
+      (const bf16 *)logits, (int)experts, (int)topk, renormalize, topk_weights, topk_ids);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+extern "C" int lm_moe_align(const int32_t *ids, int64_t routes, int64_t first_expert,
+                            int64_t local_experts, int32_t *expert_offsets, int32_t *sorted_routes,
+                            int32_t *inverse, void *stream) {
+  LM_REQUIRE(routes >= 0 && routes < (int64_t)1 << 30 && local_experts > 0 && first_expert >= 0);
+  if (local_experts > kMaxAlignExperts) return LM_EUNSUPPORTED;
+  LM_REQUIRE(expert_offsets && (routes == 0 || (ids && sorted_routes)));
+  const size_t shmem = sizeof(int) * ((size_t)kAlignWaves * (local_experts + 1) + 2 * kAlignThreads);
+  align_kernel<<<1, kAlignThreads, shmem, (hipStream_t)stream>>>(
+      ids, (int)routes, (int)first_expert, (int)local_experts, expert_offsets, sorted_routes,
+      inverse);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}

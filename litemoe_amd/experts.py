@@ -1,0 +1,131 @@
+"""Expert backend on the gfx950 kernels: the drop-in for vLLM ``fused_experts``.
+
+``HipFusedExperts`` follows the reference's backend protocol
+(litemoe/vllm_moe.py:6-27, ops.py:59-61): attributes ``graph_safe``, ``name``,
+``fused_combine``; ``operation(x, w1, w2, topk_weights, topk_ids,
+apply_router_weight_on_input=False, global_num_experts=E)`` as the lean EP1
+path calls it (ep.py:40-41); ``__call__(x, ids, scales, w1, w2, rank, world,
+out, logical=None)`` writing into ``out``. The model gates its fused decode
+path on the ``native`` capability attribute instead of a type check.
+"""
+import torch
+
+from . import _lib
+
+
+def _check_weights(x, w1, w2):
+    if any(t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous() for t in (x, w1, w2)):
+        raise ValueError('Contiguous CUDA BF16 activations/weights/output required')
+    experts, two_inter, hidden = w1.shape
+    if x.shape[-1] != hidden or w2.shape != (experts, hidden, two_inter // 2) or two_inter % 2:
+        raise ValueError('Expert weight shapes must be w1 [E, 2I, H] and w2 [E, H, I]')
+    return experts, hidden, two_inter // 2
+
+
+class _Workspace:
+    """Grow-only device scratch; allocated before graph capture, then reused."""
+
+    def __init__(self):
+        self.buffers = {}
+
+    def get(self, device, nbytes):
+        key = (str(device),)
+        buf = self.buffers.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self.buffers[key] = buf
+        return buf
+
+
+_SHARED = _Workspace()
+
+
+def fused_experts(x, w1, w2, topk_weights, topk_ids, apply_router_weight_on_input=False,
+                  global_num_experts=None, out=None, logical=None, block_rows=0, workspace=None):
+    """``out[t] = sum_j w[t,j] * W2[e] (silu(W13[e,:I] x_t) * W13[e,I:] x_t)``."""
+    if apply_router_weight_on_input:
+        raise ValueError('apply_router_weight_on_input=True is not implemented')
+    experts, hidden, inter = _check_weights(x, w1, w2)
+    if global_num_experts is not None and global_num_experts != experts:
+        raise ValueError('Expert parallelism is not part of this single-GPU path')
+    tokens = x.numel() // hidden
+    topk = topk_ids.shape[-1]
+    if topk_ids.shape[0] != tokens or topk_weights.shape != topk_ids.shape:
+        raise ValueError('Router outputs must be [tokens, topk]')
+    ids = topk_ids.to(torch.int32).contiguous()
+    weights = topk_weights.to(torch.float32).contiguous()
+    out = torch.empty_like(x) if out is None else out
+    if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+        raise ValueError('Output must match x')
+    remap = logical is not None and logical.numel() != 0
+    logical64 = logical.to(torch.int64).contiguous() if remap else None
+    nbytes = _lib.size_query("lm_fused_experts_workspace_size", tokens, topk, hidden, inter, experts)
+    ws = (workspace or _SHARED).get(x.device, nbytes)
+    _lib.call("lm_fused_experts", x.data_ptr(), w1.data_ptr(), w2.data_ptr(), weights.data_ptr(),
+              ids.data_ptr(), _lib.ptr(logical64), tokens, hidden, inter, experts, topk, block_rows,
+              out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(x.device))
+    return out
+
+
+class HipFusedExperts:
+    graph_safe = True
+    name = 'hip-gfx950-fused-experts'
+    fused_combine = True
+    native = True  # capability the model's fused decode path is gated on
+
+    def __init__(self, block_rows=0):
+        self.block_rows = block_rows
+        self.workspace = _Workspace()
+
+    def operation(self, x, w1, w2, topk_weights, topk_ids, apply_router_weight_on_input=False,
+                  global_num_experts=None, out=None):
+        return fused_experts(x, w1, w2, topk_weights, topk_ids, apply_router_weight_on_input,
+                             global_num_experts, out=out, block_rows=self.block_rows,
+                             workspace=self.workspace)
+
+    def __call__(self, x, ids, scales, w1, w2, rank, world, out, logical=None):
+        if rank != 0 or world != 1:
+            raise ValueError('The fused-expert backend supports EP1 only')
+        if any(t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous() for t in (x, w1, w2, out)):
+            raise ValueError('Contiguous CUDA BF16 activations/weights/output required')
+        return fused_experts(x, w1, w2, scales.float(), ids.int(), out=out, logical=logical,
+                             block_rows=self.block_rows, workspace=self.workspace)
+
+
+def moe_align(topk_ids, local_experts, first_expert=0, inverse=True):
+    """Stable expert-sorted permutation of the flat routes.
+
+    Returns ``offsets [E+1]`` (int32), ``sorted_routes`` (int32, equal to
+    ``argsort(key, stable=True)``) and optionally ``inverse``; non-local routes
+    sort into the tail after ``offsets[E]`` (litemoe/ops.py:163-173).
+    """
+    _lib.require_cuda(topk_ids, what="expert ids")
+    ids = topk_ids.to(torch.int32).contiguous().view(-1)
+    routes = ids.numel()
+    offsets = torch.empty(local_experts + 1, device=ids.device, dtype=torch.int32)
+    order = torch.empty(routes, device=ids.device, dtype=torch.int32)
+    inv = torch.empty(routes, device=ids.device, dtype=torch.int32) if inverse else None
+    _lib.call("lm_moe_align", ids.data_ptr(), routes, first_expert, local_experts, offsets.data_ptr(),
+              order.data_ptr(), _lib.ptr(inv), _lib.stream(ids.device))
+    return offsets, order, inv
+
+
+def gate_up(x, w1, offsets, sorted_routes, topk, block_rows=0):
+    """Stage 1: ``act[p] = bf16(silu(bf16(g)) * bf16(u))`` per sorted route."""
+    experts, hidden, inter = _check_weights(x, w1, torch.empty(w1.shape[0], w1.shape[2], w1.shape[1] // 2,
+                                                              device=x.device, dtype=x.dtype))
+    routes = sorted_routes.numel()
+    act = torch.zeros(routes, inter, device=x.device, dtype=x.dtype)
+    _lib.call("lm_moe_gate_up", x.data_ptr(), w1.data_ptr(), offsets.data_ptr(), sorted_routes.data_ptr(),
+              routes, topk, hidden, inter, experts, block_rows, act.data_ptr(), _lib.stream(x.device))
+    return act
+
+
+def down(act, w2, offsets, sorted_routes, block_rows=0):
+    """Stage 2: ``y[sorted[p]] = bf16(W2[e] . act[p])`` in route order."""
+    experts, hidden, inter = w2.shape
+    routes = sorted_routes.numel()
+    y = torch.zeros(routes, hidden, device=act.device, dtype=act.dtype)
+    _lib.call("lm_moe_down", act.data_ptr(), w2.data_ptr(), offsets.data_ptr(), sorted_routes.data_ptr(),
+              routes, hidden, inter, experts, block_rows, y.data_ptr(), _lib.stream(act.device))
+    return y

@@ -1,0 +1,54 @@
+"""Graph-safe split-K decode attention over each row's contiguous KV sequence.
+
+Mirrors ``FlashDecode`` of litemoe/flash_decode.py:5-34: built once per
+(batch, kv_heads, groups, capacity), called with ``q [B, Hq, 1, D]`` and the
+layer caches ``k, v [B, Hkv, C, D]``; row b attends keys ``j < used[b]``
+(``used = where(active, lengths + 1, 1)`` unless given). The split count is
+fixed at construction, so the launch is capturable.
+"""
+import math
+
+import torch
+
+from . import _lib
+
+
+def default_splits(batch, kv_heads, maximum, keys_per_split=256, max_splits=16):
+    """Enough splits to fill the GPU at short contexts, chunks of ~256 keys."""
+    return max(1, min(max_splits, math.ceil(maximum / keys_per_split)))
+
+
+class FlashDecode:
+    def __init__(self, batch, kv_heads, groups, capacity, device, maximum=None, num_splits=None):
+        if maximum is not None and not 0 < maximum <= capacity:
+            raise ValueError("Decode attention requires a valid length bound")
+        self.batch, self.kv_heads, self.groups, self.capacity = batch, kv_heads, groups, capacity
+        self.maximum = capacity if maximum is None else maximum
+        self.splits = num_splits or default_splits(batch, kv_heads, self.maximum)
+        self.device = torch.device(device)
+        size = _lib.size_query("lm_flash_decode_workspace_size", batch, kv_heads * groups, 64,
+                               self.splits) if self.device.type == "cuda" else 0
+        self.workspace = torch.empty(max(size, 1), dtype=torch.uint8, device=self.device)
+
+    def __call__(self, q, k, v, lengths, active, scale, used=None):
+        b, hq, s, d = q.shape
+        if s != 1 or d != 64:
+            raise ValueError("Decode attention takes one query position with head_dim 64")
+        if k.shape != v.shape or k.shape[0] != b or k.shape[3] != d or hq % k.shape[1]:
+            raise ValueError("KV cache layer shape does not match the queries")
+        if b > self.batch or k.shape[2] != self.capacity:
+            raise ValueError("Decode attention built for another batch/capacity")
+        _lib.require_cuda(q, k, v, what="decode attention tensors")
+        if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+            raise ValueError("Decode attention supports BF16")
+        if q.stride(3) != 1 or not k.is_contiguous() or not v.is_contiguous():
+            raise ValueError("Decode attention needs contiguous channels and cache layers")
+        if used is None:
+            used = torch.where(active, lengths + 1, 1).to(torch.int32)
+        used = used.to(torch.int32).contiguous()
+        out = torch.empty(b, hq, 1, d, device=q.device, dtype=q.dtype)
+        _lib.call("lm_flash_decode", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                  used.data_ptr(), b, hq, k.shape[1], self.capacity, d, float(scale), self.maximum,
+                  self.splits, out.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(),
+                  _lib.stream(q.device))
+        return out

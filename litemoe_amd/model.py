@@ -1,0 +1,132 @@
+"""Granite MoE forward on the gfx950 kernels (litemoe/model.py:17-127).
+
+``Granite(cfg, weights, ep, capacity).forward(tokens, positions, valid, cache,
+slot=None, last=None, communication_tokens=None)`` keeps the reference's
+signature and tensor layouts. Per layer (decode and packed prefill alike):
+
+    x += r * y_prev; z = rmsnorm(x)          lm_add_rmsnorm (layer 0: plain norm)
+    qkv = z . Wqkv^T                         hipBLASLt (packed q|k|v, model.py:37-40,47-49)
+    rope(q, k); k, v -> cache                lm_rope_kv_write
+    a = attention(q, cache or packed k/v)    lm_flash_decode | lm_prefill_attention
+    a = a . Wo^T                             hipBLASLt
+    x += r * a; z = rmsnorm(x)               lm_add_rmsnorm
+    w, ids = router(z)                       lm_router (GEMV + top-k + softmax)
+    y = experts(z, ids, w)                   lm_fused_experts (align, gate_up, down, finish)
+
+then ``x += r * y; logits = rmsnorm(x) . head^T / logits_scaling``. Dense
+projections stay on the vendor BLAS for now; every other step is a
+hand-written kernel. There is no CPU path: inputs must be on the GPU.
+"""
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .config import validate_config
+from .flash_decode import FlashDecode
+from .norm import add_rmsnorm
+from .packed import PackedPrefill, varlen_attention
+from .rope import rope_kv_write
+from .router import route
+
+
+class Granite:
+    def __init__(self, cfg, weights, ep, capacity):
+        validate_config(cfg)
+        self.cfg, self.w, self.ep = cfg, weights, ep
+        self.trace = None
+        self.decode_flash = None   # FlashDecode set by the execution policy
+        self.decode_lean = False   # positions pre-zeroed for stopped rows; outputs unmasked
+        self.used = None
+        self._flash = {}
+        device, dtype = weights["embedding"].device, weights["embedding"].dtype
+        dim = cfg.hidden_size // cfg.num_attention_heads
+        self.capacity = capacity
+        # RoPE tables as litemoe/model.py:31-36: inverse frequencies on the CPU
+        # in fp32 (HF's initialisation), positions on the device.
+        inv = 1.0 / cfg.rope_theta ** (torch.arange(0, dim, 2, device="cpu").float() / dim)
+        freq = torch.outer(torch.arange(capacity, device=device).float(), inv.to(device))
+        self.cos_sin = torch.cat((freq.cos(), freq.sin()), -1).to(dtype)
+        self.cos, self.sin = [half.repeat(1, 2) for half in self.cos_sin.chunk(2, -1)]
+        self.prepare_packed_qkv()
+
+    def prepare_packed_qkv(self):
+        for w in self.w["layers"]:
+            if "self_attn.qkv_proj" not in w:
+                w["self_attn.qkv_proj"] = torch.cat([w[f"self_attn.{p}_proj"] for p in ("q", "k", "v")])
+
+    def _decode_attention(self, batch, cache):
+        if self.decode_flash is not None:
+            return self.decode_flash
+        key = (batch, cache.capacity)
+        if key not in self._flash:
+            cfg = self.cfg
+            self._flash[key] = FlashDecode(batch, cfg.num_key_value_heads,
+                                           cfg.num_attention_heads // cfg.num_key_value_heads,
+                                           cache.capacity, cache.k.device)
+        return self._flash[key]
+
+    def attention(self, z, w, cache, layer, rope_positions, active, positions, slot):
+        """Packed QKV projection, RoPE + KV store, attention, output projection
+        (litemoe/model.py:42-73). ``z [rows, H]`` -> ``[rows, H]``."""
+        cfg = self.cfg
+        rows = z.shape[0]
+        d = cfg.hidden_size // cfg.num_attention_heads
+        hq, hkv = cfg.num_attention_heads, cfg.num_key_value_heads
+        qkv = F.linear(z, w["self_attn.qkv_proj"])
+        q = qkv[:, :hq * d].view(rows, hq, d)
+        k = qkv[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
+        v = qkv[:, (hq + hkv) * d:].view(rows, hkv, d)
+        packed = isinstance(slot, PackedPrefill)
+        rope_kv_write(q, k, v, rope_positions, active, self.cos_sin, cache, layer,
+                      slots=slot.slots if packed else None, write_k=packed)
+        if packed:
+            a = varlen_attention(q, k, v, slot.cu, slot.maximum, cfg.attention_multiplier)
+        else:
+            flash = self._decode_attention(rows, cache)
+            a = flash(q.unsqueeze(2), cache.k[layer], cache.v[layer], positions, active,
+                      cfg.attention_multiplier, self.used)
+        return F.linear(a.reshape(rows, hq * d), w["self_attn.o_proj"])
+
+    def forward(self, tokens, positions, valid, cache, slot=None, last=None, communication_tokens=None):
+        cfg = self.cfg
+        packed = isinstance(slot, PackedPrefill)
+        if slot is not None and not packed:
+            raise ValueError("Prefill on this path is packed (use packed_prefill_logits)")
+        _lib.require_cuda(tokens, positions, valid, cache.k, what="model inputs")
+        b, s = tokens.shape
+        hidden, eps, r = cfg.hidden_size, cfg.rms_norm_eps, cfg.residual_multiplier
+        valid_rows = valid.reshape(-1)
+        if packed:
+            rope_positions, flat_positions = slot.positions, slot.positions
+            self.used = None
+        else:
+            if s != 1:
+                raise ValueError("Decode takes one token per row")
+            flat_positions = positions[:, 0]
+            lean = self.decode_lean
+            rope_positions = flat_positions if lean else torch.where(valid_rows, flat_positions, 0)
+            # seqused_k of flash_decode.py:21 / model.py:103
+            self.used = ((rope_positions + 1) if lean else
+                         torch.where(valid_rows, flat_positions + 1, 1)).to(torch.int32)
+        masked = not packed and not self.decode_lean
+        x = (F.embedding(tokens, self.w["embedding"]) * cfg.embedding_multiplier).reshape(b * s, hidden)
+        x = x.contiguous()
+        z = torch.empty_like(x)
+        y = None
+        for layer, w in enumerate(self.w["layers"]):
+            add_rmsnorm(x, y, r, w["input_layernorm"], eps, out=z)
+            a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
+            if masked:
+                a = a * valid_rows[:, None]
+            add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps, out=z)
+            scales, ids = route(z, w["block_sparse_moe.router.layer"], cfg.num_experts_per_tok)
+            y = self.ep(z, ids, scales, valid_rows, w["physical"], w["input_linear"], w["output_linear"],
+                        w["logical"], decode=True, tokens=communication_tokens)
+        if last is not None:
+            index = last.long() if isinstance(last, torch.Tensor) else torch.tensor([last], device=x.device)
+            x, y = x[index].contiguous(), y[index].contiguous()
+            out_rows = (x.shape[0], 1)
+        else:
+            out_rows = (b, s)
+        z = add_rmsnorm(x, y, r, self.w["norm"], eps)
+        return (F.linear(z, self.w["head"]) / cfg.logits_scaling).view(*out_rows, -1)

@@ -1,0 +1,53 @@
+"""Router: gate GEMV, top-k and softmax on the gfx950 kernel.
+
+``fused_topk`` keeps vLLM's signature as the reference calls it
+(litemoe/model.py:112-113): ``fused_topk(hidden, gating_output, topk,
+renormalize=True) -> (weights fp32 [M,k], ids int32 [M,k], indices)``.
+``route`` fuses the router GEMV ``linear_rows(z, router.layer)``
+(model.py:110) in front of it. Selection: descending logits, equal logits by
+ascending expert id.
+"""
+import torch
+
+from . import _lib
+
+
+def _outputs(m, topk, device):
+    return (torch.empty(m, topk, device=device, dtype=torch.float32),
+            torch.empty(m, topk, device=device, dtype=torch.int32))
+
+
+def fused_topk(hidden_states, gating_output, topk, renormalize=True):
+    """Top-k of bf16 logits ``gating_output [M, E]``. The third output is the
+    flat route index ``t * topk + j`` of each selection."""
+    _lib.require_cuda(gating_output, what="router logits")
+    if gating_output.dtype != torch.bfloat16 or gating_output.ndim != 2:
+        raise ValueError('Router logits must be a BF16 [tokens, experts] tensor')
+    if hidden_states is not None and hidden_states.shape[0] != gating_output.shape[0]:
+        raise ValueError('Hidden states and logits disagree on the token count')
+    logits = gating_output.contiguous()
+    m, experts = logits.shape
+    weights, ids = _outputs(m, topk, logits.device)
+    _lib.call("lm_topk_softmax", logits.data_ptr(), m, experts, topk, int(bool(renormalize)),
+              weights.data_ptr(), ids.data_ptr(), _lib.stream(logits.device))
+    indices = torch.arange(m * topk, device=logits.device, dtype=torch.int32).view(m, topk)
+    return weights, ids, indices
+
+
+def route(z, gate_weight, topk, renormalize=True, logits_out=None):
+    """Fused ``logits = bf16(z . W_r^T)`` then ``fused_topk``; ``z [M, H]``,
+    ``gate_weight [E, H]``. Optionally writes the bf16 logits."""
+    _lib.require_cuda(z, gate_weight, what="router inputs")
+    if z.dtype != torch.bfloat16 or gate_weight.dtype != torch.bfloat16:
+        raise ValueError('Router supports BF16')
+    if not z.is_contiguous() or not gate_weight.is_contiguous() or z.shape[-1] != gate_weight.shape[1]:
+        raise ValueError('Router needs contiguous [M, H] input and [E, H] weight')
+    m, hidden = z.numel() // z.shape[-1], z.shape[-1]
+    experts = gate_weight.shape[0]
+    weights, ids = _outputs(m, topk, z.device)
+    if logits_out is not None and (logits_out.shape != (m, experts) or logits_out.dtype != torch.bfloat16):
+        raise ValueError('logits_out must be BF16 [tokens, experts]')
+    _lib.call("lm_router", z.data_ptr(), gate_weight.data_ptr(), m, hidden, experts, topk,
+              int(bool(renormalize)), _lib.ptr(logits_out), weights.data_ptr(), ids.data_ptr(),
+              _lib.stream(z.device))
+    return weights, ids

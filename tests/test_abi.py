@@ -1,0 +1,61 @@
+"""The C-ABI library loads, exports every symbol include/litemoe_amd.h
+declares, and its host-side checks work without a GPU (no kernel launches)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from litemoe_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "litemoe_amd.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|const char \*)\s*(lm_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    handle = _lib.load()
+    names = declared()
+    assert len(names) >= 15
+    assert sorted(_lib.EXPORTED) == names
+    for name in names:
+        assert hasattr(handle, name), name
+
+
+def test_version_and_status_strings():
+    handle = _lib.load()
+    assert b"gfx950" in handle.lm_version()
+    assert handle.lm_status_string(0) == b"ok"
+    assert handle.lm_status_string(4) == b"workspace too small"
+
+
+def test_workspace_queries():
+    # tokens 64, top-8, hidden 1536, inter 512, 40 experts (the 3B decode shape)
+    size = _lib.size_query("lm_fused_experts_workspace_size", 64, 8, 1536, 512, 40)
+    routes = 64 * 8
+    assert size == 256 + 4 * routes + 2 * routes * 512 + 2 * routes * 1536
+    assert _lib.size_query("lm_flash_decode_workspace_size", 64, 24, 64, 1) == 0
+    n = 64 * 24 * 5
+    assert _lib.size_query("lm_flash_decode_workspace_size", 64, 24, 64, 5) == n * 256 + 2 * n * 4
+
+
+@pytest.mark.parametrize("call,expected", [
+    (lambda h: h.lm_rmsnorm(None, None, None, -1, 16, C.c_float(1e-6), None), 1),
+    (lambda h: h.lm_flash_decode(None, 0, 0, None, None, None, 1, 4, 2, 8, 128, C.c_float(1.0), 8, 1, None, None,
+                                 0, None), 2),
+    (lambda h: h.lm_moe_align(None, 4, 0, 600, None, None, None, None), 2),
+    (lambda h: h.lm_fused_experts(None, None, None, None, None, None, 4, 1000, 512, 8, 2, 0, None, None, 0, None), 2),
+    (lambda h: h.lm_moe_finish(None, None, None, None, None, None, 1, 8, 9, 0, 1, None, 0, None), 1),
+    (lambda h: h.lm_router(None, None, 2, 1536, 300, 8, 1, None, None, None, None), 2),
+])
+def test_invalid_arguments_rejected_on_host(call, expected):
+    assert call(_lib.load()) == expected
+
+
+def test_single_hip_runtime_in_process():
+    import torch  # noqa: F401  (loads torch's HIP runtime)
+    _lib.load()
+    _lib._check_single_runtime()

@@ -1,0 +1,385 @@
+"""Kernel-level parity of the gfx950 path against the CPU oracle.
+
+Bars: bit-exact for integer/index work (top-k ids given logits, the route
+permutation, KV stores, RoPE, the combine given y); floating point within the
+tolerances written in each test (the reference's own where it has one,
+otherwise the rel-L2 <= 2e-2 of the north star).
+"""
+import pytest
+import torch
+
+from helpers import rel_l2
+from litemoe_amd import experts, flash_decode, kv_write, moe_finish, norm, packed, rope, router
+from litemoe_amd.cache import KVCache
+from litemoe_amd.config import ModelConfig
+from litemoe_amd.synth import normal_bf16
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def bf(shape, std=1.0, seed=0):
+    return normal_bf16(shape, std, seed)
+
+
+def ulp_diff(a, b):
+    """Max distance in bf16 units in the last place (same-sign values)."""
+    ai = a.contiguous().view(torch.int16).to(torch.int32)
+    bi = b.contiguous().view(torch.int16).to(torch.int32)
+    return int((ai - bi).abs().max()) if a.numel() else 0
+
+
+# ------------------------------------------------------------------- norms --
+
+@pytest.mark.parametrize("shape", [(1, 1, 1536), (8, 1, 2048), (32, 1, 3072), (2, 1, 33), (64, 1, 1536)])
+@torch.inference_mode()
+def test_rmsnorm_matches_oracle(shape):
+    x = bf(shape, 1.0, 1)
+    w = (1 + 0.2 * bf(shape[-1:], 1.0, 2).float()).to(torch.bfloat16)
+    for scale in (0.0, 1e-3, 1.0, 1e3):
+        xs = (x.float() * scale).to(torch.bfloat16)
+        got = norm.rmsnorm(xs.to(DEV), w.to(DEV), 1e-6).cpu()
+        exp = ops.rmsnorm(xs, w, 1e-6)
+        torch.testing.assert_close(got, exp, atol=.016, rtol=.008)  # reference test_fused_norm.py:97
+        if scale:
+            assert rel_l2(got, exp) < .005
+            assert (got != exp).float().mean() < 0.01  # rsqrt rounding flips at most a few ulps
+
+
+@torch.inference_mode()
+def test_add_rmsnorm_updates_residual_and_normalises():
+    x = bf((64, 1536), 1.0, 3)
+    a = bf((64, 1536), 1.0, 4)
+    w = (1 + 0.2 * bf((1536,), 1.0, 5).float()).to(torch.bfloat16)
+    xd = x.to(DEV)
+    y = norm.add_rmsnorm(xd, a.to(DEV), 0.22, w.to(DEV), 1e-6).cpu()
+    x_new = x.add(a, alpha=0.22)
+    assert ulp_diff(xd.cpu(), x_new) <= 1 and (xd.cpu() != x_new).float().mean() < 1e-3
+    torch.testing.assert_close(y, ops.rmsnorm(xd.cpu(), w, 1e-6), atol=.016, rtol=.008)
+
+
+# ---------------------------------------------------------------- kv store --
+
+@pytest.mark.parametrize("capacity", [8, 4096])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@torch.inference_mode()
+def test_kv_write_bitwise_strided_inactive_and_graph(capacity, dtype):
+    """Reference test_fused_kv_write.py:7-46."""
+    cfg = ModelConfig(num_key_value_heads=3, hidden_size=21, num_attention_heads=3, num_hidden_layers=2)
+    cache = KVCache(cfg, 3, capacity, DEV, dtype)
+    cache.k.normal_()
+    cache.v.normal_()
+    k = torch.randn(3, 3, 1, 28, device=DEV, dtype=dtype)[..., ::4]
+    v = torch.randn(3, 3, 1, 42, device=DEV, dtype=dtype)[..., 1::6]
+    pos = torch.tensor([0, capacity + 10, capacity - 1], device=DEV)
+    active = torch.tensor([True, False, True], device=DEV)
+    k[1].fill_(float("nan"))
+    v[1].fill_(float("nan"))
+    expected_k, expected_v = cache.k.clone(), cache.v.clone()
+    for slot, p in ((0, 0), (2, capacity - 1)):
+        expected_k[1, slot, :, p] = k[slot, :, 0]
+        expected_v[1, slot, :, p] = v[slot, :, 0]
+    cache.write(1, k, v, pos, active)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k, expected_k) and torch.equal(cache.v, expected_v)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cache.write(1, k, v, pos, active)
+    for replay in range(3):
+        pos.copy_(torch.tensor([1 + replay, 2 + replay, capacity + 99], device=DEV))
+        active.copy_(torch.tensor([True, True, False], device=DEV))
+        k.normal_()
+        v.normal_()
+        for slot in (0, 1):
+            expected_k[1, slot, :, 1 + replay + slot] = k[slot, :, 0]
+            expected_v[1, slot, :, 1 + replay + slot] = v[slot, :, 0]
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cache.k, expected_k) and torch.equal(cache.v, expected_v)
+
+
+# -------------------------------------------------------------------- rope --
+
+@torch.inference_mode()
+def test_rope_bitwise_on_packed_views():
+    """Rotation equals the torch formula of model.py:66-67 bit for bit on
+    strided views of a packed QKV buffer (vLLM entry, model.py:63-64)."""
+    t, hq, hkv, d = 37, 24, 8, 64
+    cos_sin, cos, sin = ops.rope_tables(1e4, d, 4096, torch.bfloat16)
+    qkv = bf((t, (hq + 2 * hkv) * d), 1.0, 6)
+    pos = torch.randint(0, 4096, (t,))
+    dev = qkv.to(DEV)
+    q = dev[:, :hq * d].view(t, hq, d)
+    k = dev[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    rope.rotary_embedding(pos.to(DEV), q, k, d, cos_sin.to(DEV))
+    eq = ops.rope(qkv[:, :hq * d].view(t, hq, d), cos, sin, pos)
+    ek = ops.rope(qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d), cos, sin, pos)
+    assert torch.equal(q.cpu(), eq) and torch.equal(k.cpu(), ek)
+    assert torch.equal(dev[:, (hq + hkv) * d:].cpu(), qkv[:, (hq + hkv) * d:])  # v untouched
+
+
+@pytest.mark.parametrize("write_k", [False, True])
+@torch.inference_mode()
+def test_rope_kv_write_stores_rotated_k_and_v(write_k):
+    t, hq, hkv, d, cap = 9, 6, 2, 64, 32
+    cfg = ModelConfig(num_key_value_heads=hkv, hidden_size=hq * d, num_attention_heads=hq, num_hidden_layers=2)
+    cache = KVCache(cfg, 4, cap, DEV, torch.bfloat16)
+    cache.k.normal_()
+    cache.v.normal_()
+    before_k, before_v = cache.k.cpu(), cache.v.cpu()
+    cos_sin, cos, sin = ops.rope_tables(1e4, d, cap, torch.bfloat16)
+    qkv = bf((t, (hq + 2 * hkv) * d), 1.0, 7)
+    pos = torch.tensor([0, 1, 2, 31, 5, 40, 7, 3, 4])
+    active = torch.tensor([True, True, True, True, False, True, True, True, True])
+    slots = torch.tensor([0, 0, 0, 3, 1, 2, 9, 1, 1])  # slot 9 and position 40 out of range: skipped
+    dev = qkv.to(DEV)
+    q = dev[:, :hq * d].view(t, hq, d)
+    k = dev[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    v = dev[:, (hq + hkv) * d:].view(t, hkv, d)
+    rope.rope_kv_write(q, k, v, pos.to(DEV), active.to(DEV), cos_sin.to(DEV), cache, 1, slots.to(DEV), write_k)
+    rk = ops.rope(qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d), cos, sin, pos.clamp(max=cap - 1))
+    rv = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    ek, ev = ops.kv_store(before_k[1], before_v[1], rk, rv, pos, active, slots)
+    assert torch.equal(cache.k[1].cpu(), ek) and torch.equal(cache.v[1].cpu(), ev)
+    assert torch.equal(cache.k[0].cpu(), before_k[0])
+    assert torch.equal(q.cpu()[:5], ops.rope(qkv[:5, :hq * d].view(5, hq, d), cos, sin, pos[:5]))
+    if write_k:
+        assert torch.equal(k.cpu()[:5], rk[:5])
+    else:
+        assert torch.equal(k.cpu(), qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d))
+
+
+# ------------------------------------------------------------------ router --
+
+@pytest.mark.parametrize("m,h,e,k", [(16, 1024, 32, 8), (64, 1536, 40, 8), (4096, 1536, 40, 8), (7, 256, 8, 2)])
+@torch.inference_mode()
+def test_router_ids_bit_exact_given_logits(m, h, e, k):
+    z = bf((m, h), 1.0, 10 + m)
+    wr = bf((e, h), 0.02 * 8, 20 + m)
+    logits = torch.empty(m, e, device=DEV, dtype=torch.bfloat16)
+    weights, ids = router.route(z.to(DEV), wr.to(DEV), k, logits_out=logits)
+    logits = logits.cpu()
+    cpu_logits = torch.nn.functional.linear(z, wr)
+    # GEMV accumulation order differs from the CPU BLAS: a logit may move by
+    # one bf16 ulp, rarely.
+    assert ulp_diff(logits, cpu_logits) <= 1
+    assert (logits != cpu_logits).float().mean() < 0.02
+    ew, eids = ops.route(logits, k)
+    assert torch.equal(ids.cpu(), eids)
+    torch.testing.assert_close(weights.cpu(), ew, rtol=2e-6, atol=1e-7)
+    # end to end: every id mismatch must come with a logit difference
+    _, cpu_ids = ops.route(cpu_logits, k)
+    bad = (cpu_ids != ids.cpu()).any(-1)
+    assert bool(((logits != cpu_logits).any(-1) | ~bad).all())
+
+
+@pytest.mark.parametrize("renormalize", [True, False])
+@torch.inference_mode()
+def test_topk_softmax_ties_go_to_lower_id(renormalize):
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randint(-3, 4, (300, 40), generator=g).to(torch.bfloat16)
+    weights, ids, idx = router.fused_topk(None, logits.to(DEV), 8, renormalize=renormalize)
+    ew, eids = ops.route(logits, 8, renormalize=renormalize)
+    assert torch.equal(ids.cpu(), eids)
+    torch.testing.assert_close(weights.cpu(), ew, rtol=2e-6, atol=1e-7)
+    assert torch.equal(idx.cpu().flatten(), torch.arange(300 * 8, dtype=torch.int32))
+
+
+# ------------------------------------------------------------- permutation --
+
+@pytest.mark.parametrize("m,k,e,first,local", [(64, 8, 40, 0, 40), (16, 8, 32, 0, 32), (4096, 8, 40, 0, 40),
+                                                (64, 8, 40, 10, 5), (1, 1, 4, 0, 4), (50000, 8, 40, 0, 40)])
+@torch.inference_mode()
+def test_moe_align_bit_exact(m, k, e, first, local):
+    g = torch.Generator().manual_seed(m + first)
+    ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(m)]).to(torch.int32) if m < 5000 else \
+        torch.randint(0, e, (m, k), generator=g, dtype=torch.int32)
+    offsets, order, inverse = experts.moe_align(ids.to(DEV), local, first)
+    eo, eord, einv = ops.permutation(ids, local, first)
+    assert offsets.cpu().tolist() == eo.tolist()
+    assert torch.equal(order.cpu().long(), eord)
+    assert torch.equal(inverse.cpu().long(), einv)
+
+
+@torch.inference_mode()
+def test_moe_align_skewed():
+    g = torch.Generator().manual_seed(9)
+    hot = torch.randint(0, 4, (20000, 8), generator=g)
+    cold = torch.randint(0, 40, (20000, 8), generator=g)
+    ids = torch.where(torch.rand(20000, 8, generator=g) < 0.5, hot, cold).to(torch.int32)
+    offsets, order, _ = experts.moe_align(ids.to(DEV), 40)
+    eo, eord, _ = ops.permutation(ids, 40)
+    assert offsets.cpu().tolist() == eo.tolist() and torch.equal(order.cpu().long(), eord)
+
+
+# ----------------------------------------------------------------- experts --
+
+def _moe_inputs(m, h, i, e, k, seed):
+    x = bf((m, h), 1.0, seed)
+    w1 = bf((e, 2 * i, h), 0.02, seed + 1)
+    w2 = bf((e, h, i), 0.02, seed + 2)
+    wr = bf((e, h), 0.02, seed + 3)
+    weights, ids = ops.route(torch.nn.functional.linear(x, wr), k)
+    return x, w1, w2, weights, ids
+
+
+@pytest.mark.parametrize("m,h,i,e,k", [(16, 1024, 512, 32, 8), (64, 1536, 512, 40, 8), (5, 1536, 512, 40, 8),
+                                       (300, 1024, 512, 32, 8), (64, 256, 128, 8, 2)])
+@torch.inference_mode()
+def test_expert_stages_match_oracle(m, h, i, e, k):
+    x, w1, w2, weights, ids = _moe_inputs(m, h, i, e, k, 100 + m)
+    offsets, order, _ = experts.moe_align(ids.to(DEV), e)
+    act = experts.gate_up(x.to(DEV), w1.to(DEV), offsets, order, k).cpu()
+    order_c = order.cpu().long()
+    rows = x[order_c // k]
+    exp_act = torch.empty_like(act)
+    for p in range(order_c.numel()):
+        ex = int(ids.flatten()[order_c[p]])
+        gate, up = torch.nn.functional.linear(rows[p:p + 1], w1[ex]).chunk(2, -1)
+        exp_act[p] = (torch.nn.functional.silu(gate) * up)[0]
+    assert rel_l2(act, exp_act) < 5e-3
+    y = experts.down(act.to(DEV), w2.to(DEV), offsets, order).cpu()
+    ey = ops.expert_routes(x, ids, w1, w2)
+    assert rel_l2(y, ey) < 1e-2
+
+
+@pytest.mark.parametrize("m,h,i,e,k", [(16, 1024, 512, 32, 8), (64, 1536, 512, 40, 8), (1, 1536, 512, 40, 8),
+                                       (512, 1536, 512, 40, 8)])
+@torch.inference_mode()
+def test_fused_experts_match_oracle(m, h, i, e, k):
+    x, w1, w2, weights, ids = _moe_inputs(m, h, i, e, k, 200 + m)
+    out = experts.fused_experts(x.to(DEV), w1.to(DEV), w2.to(DEV), weights.to(DEV), ids.to(DEV)).cpu()
+    expected = ops.fused_moe(x, ids, weights, w1, w2)
+    assert rel_l2(out, expected) < 1e-2          # north-star bar 2e-2
+    reference = ops.reference_experts(x, ids, weights.to(torch.bfloat16).float(), w1, w2, singleton=True)
+    assert rel_l2(out, reference) < 2e-2          # the reference CPU path
+
+
+@torch.inference_mode()
+def test_fused_experts_block_rows_do_not_change_results():
+    x, w1, w2, weights, ids = _moe_inputs(200, 1024, 512, 8, 2, 7)
+    args = [t.to(DEV) for t in (x, w1, w2, weights, ids)]
+    base = experts.fused_experts(*args, block_rows=0)
+    for bm in (16, 48, 256):
+        assert torch.equal(experts.fused_experts(*args, block_rows=bm), base)
+
+
+# ------------------------------------------------------------------ finish --
+
+@pytest.mark.parametrize("batch,topk,hidden,rank,world,remap", [
+    (1, 8, 1536, 0, 1, False), (8, 8, 2048, 0, 1, True), (32, 8, 65, 1, 2, False),
+    (8, 3, 129, 0, 2, True), (1, 1, 65, 0, 1, False)])
+@torch.inference_mode()
+def test_finish_bit_exact_mask_order_and_graph(batch, topk, hidden, rank, world, remap):
+    """Reference test_moe_finish.py:20-71 cases; bit-exact vs the oracle."""
+    torch.manual_seed(29)
+    count = 8
+
+    def make():
+        ids = torch.stack([torch.randperm(count * world)[:topk] for _ in range(batch)]).int()
+        order = ids.flatten().argsort()
+        y = torch.randn(batch * topk, hidden).to(torch.bfloat16)
+        scales = torch.softmax(torch.randn(batch, topk), -1)
+        if batch > 1:
+            scales[-1] = 0
+        selected = ids.flatten()[order].long() - rank * count
+        y[(selected < 0) | (selected >= count)] = float("nan")
+        return ids, order, y, scales
+
+    logical = torch.randperm(count * world) if remap else None
+    ids, order, y, scales = make()
+    d = [t.to(DEV) for t in (ids, order, y, scales)]
+    lg = logical.to(DEV) if remap else None
+    out = torch.empty(batch, hidden, device=DEV, dtype=torch.bfloat16)
+
+    def check():
+        inverse = torch.empty_like(order)
+        inverse[order] = torch.arange(order.numel())
+        expected = ops.finish(y, ids, scales, rank, count, logical, inverse=inverse)
+        got = out.cpu()
+        assert torch.isfinite(got).all() and torch.equal(got, expected)
+        if batch > 1:
+            assert torch.count_nonzero(got[-1]) == 0
+
+    moe_finish.finish(d[2], d[0], d[1], d[3], out, rank, count, lg)
+    check()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        moe_finish.finish(d[2], d[0], d[1], d[3], out, rank, count, lg)
+    for _ in range(2):
+        ids, order, y, scales = make()
+        for dst, src in zip(d, (ids, order, y, scales)):
+            dst.copy_(src)
+        graph.replay()
+        torch.cuda.synchronize()
+        check()
+
+
+@torch.inference_mode()
+def test_finish_never_reads_all_nonlocal_nan_rows():
+    ids = torch.tensor([[0, 1, 2]], device=DEV, dtype=torch.int32)
+    y = torch.full((3, 65), float("nan"), device=DEV, dtype=torch.bfloat16)
+    out = torch.full((1, 65), float("nan"), device=DEV, dtype=torch.bfloat16)
+    moe_finish.finish(y, ids, ids.flatten().long(), torch.ones(1, 3, device=DEV), out, 1, 4)
+    assert torch.equal(out, torch.zeros_like(out))
+
+
+# --------------------------------------------------------------- attention --
+
+@pytest.mark.parametrize("b,hq,hkv,cap,low,high,splits", [
+    (64, 24, 8, 2048, 1, 1280, None), (32, 16, 8, 1024, 1, 640, 1), (5, 24, 8, 256, 1, 256, 3),
+    (128, 24, 8, 4096, 1024, 4096, None)])
+@torch.inference_mode()
+def test_flash_decode_matches_oracle(b, hq, hkv, cap, low, high, splits):
+    g = torch.Generator().manual_seed(b + cap)
+    q = torch.randn(b, hq, 64, generator=g).to(torch.bfloat16)
+    kc = torch.randn(b, hkv, cap, 64, generator=g).to(torch.bfloat16)
+    vc = torch.randn(b, hkv, cap, 64, generator=g).to(torch.bfloat16)
+    used = torch.randint(low, high + 1, (b,), generator=g, dtype=torch.int32)
+    used[0] = 1
+    fd = flash_decode.FlashDecode(b, hkv, hq // hkv, cap, DEV, maximum=high, num_splits=splits)
+    got = fd(q.to(DEV)[:, :, None], kc.to(DEV), vc.to(DEV), None, None, 0.125, used=used.to(DEV))[:, :, 0].cpu()
+    rows = list(range(min(b, 24))) + ([b - 1] if b > 24 else [])
+    exp = ops.decode_attention(q[rows], kc[rows], vc[rows], used[rows], 0.125)
+    torch.testing.assert_close(got[rows], exp, atol=.004, rtol=.03)  # reference test_flash_decode.py:53-56
+    assert rel_l2(got[rows], exp) < 5e-3
+
+
+@torch.inference_mode()
+def test_flash_decode_lengths_active_and_empty_rows():
+    b, hq, hkv, cap = 4, 6, 2, 64
+    q = torch.randn(b, hq, 1, 64, device=DEV).to(torch.bfloat16)
+    kc = torch.randn(b, hkv, cap, 64, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(b, hkv, cap, 64, device=DEV).to(torch.bfloat16)
+    fd = flash_decode.FlashDecode(b, hkv, hq // hkv, cap, DEV, maximum=63, num_splits=4)
+    lengths = torch.tensor([62, 999, 0, 10], device=DEV)
+    active = torch.tensor([True, False, True, True], device=DEV)
+    got = fd(q, kc, vc, lengths, active, 0.125)[:, :, 0].cpu()
+    used = torch.tensor([63, 1, 1, 11], dtype=torch.int32)
+    exp = ops.decode_attention(q[:, :, 0].cpu(), kc.cpu(), vc.cpu(), used, 0.125)
+    torch.testing.assert_close(got, exp, atol=.004, rtol=.03)
+    zero = fd(q, kc, vc, None, None, 0.125, used=torch.zeros(b, dtype=torch.int32, device=DEV))
+    assert torch.equal(zero, torch.zeros_like(zero))
+
+
+@pytest.mark.parametrize("lengths", [[2, 7], [1, 17, 64, 65, 130, 300], [2048, 64, 700]])
+@torch.inference_mode()
+def test_prefill_attention_matches_oracle_and_isolates_sequences(lengths):
+    t = sum(lengths)
+    g = torch.Generator().manual_seed(t)
+    hq, hkv = 24, 8
+    q = torch.randn(t, hq, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(t, hkv, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(t, hkv, 64, generator=g).to(torch.bfloat16)
+    cu = torch.tensor([0] + lengths).cumsum(0).to(torch.int32)
+    got = packed.varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), max(lengths), 0.125).cpu()
+    exp = ops.varlen_attention(q, k, v, cu, 0.125)
+    torch.testing.assert_close(got, exp, atol=.016, rtol=.016)  # reference test_packed_prefill.py:40
+    assert rel_l2(got, exp) < 1e-2
+    k2, v2 = k.clone(), v.clone()
+    k2[1] += 4
+    v2[1] += 4
+    changed = packed.varlen_attention(q.to(DEV), k2.to(DEV), v2.to(DEV), cu.to(DEV), max(lengths), 0.125).cpu()
+    assert torch.equal(changed[lengths[0]:], got[lengths[0]:])
+    assert torch.equal(changed[0], got[0])
