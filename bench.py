@@ -52,7 +52,24 @@ def parse():
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-engine", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="skip decode timing: run only the MoE kernel timing (for counter collection)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy a 256 MiB device buffer 3 times (FETCH/WRITE counter calibration)")
     return ap.parse_args()
+
+
+def measured_traffic(name):
+    """HBM bytes per launch of a kernel from its committed counter summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch="):
+                return int(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def moe_roofline(model, cfg, batch, reps):
@@ -152,6 +169,15 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.copy_probe:
+        a = torch.full((256 << 20,), 1, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("copied 3 x 256 MiB")
+        return
+
     from litemoe_amd import synth
     from litemoe_amd.config import preset
     from litemoe_amd.engine import Request
@@ -172,6 +198,12 @@ def main():
     model = Granite(cfg, w, ep, 4096)
     prompts = synth.prompts(args.batch, args.prompt, cfg.vocab_size, 1)
     requests = [Request(str(i), p, args.new_tokens) for i, p in enumerate(prompts)]
+    if args.roofline_only:
+        with torch.inference_mode():
+            roof = moe_roofline(model, cfg, args.batch, args.roofline_reps)
+        log(f"gate_up {roof['gate_up_us']:.1f} us/launch, fused MoE {roof['fused_us']:.1f} us/layer")
+        print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in roof.items()}), flush=True)
+        return
     engine = OptimizedEngine(model, requests, mode="graph", ignore_eos=True)
     with torch.inference_mode():
         t = time.perf_counter()
@@ -232,7 +264,8 @@ def main():
                    "capacity": engine.capacity, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "gate_up_kernel (lm_moe_gate_up)",
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("gate_up_kernel.granite3b_b64_decode.txt"),
                      "bytes_per_launch": int(roof["gate_up_bytes"]), "us_per_launch": round(roof["gate_up_us"], 2),
                      "active_experts": roof["active"]},
         "fused_moe": {"achieved": round(fused_gbs, 1), "unit": "GB/s", "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
