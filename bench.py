@@ -15,7 +15,7 @@ Also reported on the same JSON line:
   roofline      the dominant kernel (expert gate/up GEMM), timed with HIP
                 events on its stream over all 32 layers' weights (no cache
                 reuse across launches), against 8 TB/s;
-  fused_moe     the whole per-layer MoE (align + gate_up + down + combine);
+  fused_moe     the whole per-layer MoE (gate_up + down + combine);
   cpu_baseline  the CPU oracle (LiteMoE's torch CPU decode path restated) on a
                 bounded sample of the same decode step, extrapolated;
   engine_decode_tps  the reference's own metric from Engine.generate()
@@ -92,10 +92,10 @@ def moe_roofline(model, cfg, batch, reps):
     stream = _lib.stream(dev)
     out = torch.empty(batch, H, device=dev, dtype=torch.bfloat16)
 
-    def gate_up_all():
+    def gate_up_all():  # the decode path: each expert's workgroups collect its routes
         for w, weights, ids, offsets, order, act, _ in per_layer:
-            _lib.call("lm_moe_gate_up", z.data_ptr(), w["input_linear"].data_ptr(), offsets.data_ptr(),
-                      order.data_ptr(), batch * k, k, H, I, E, 0, act.data_ptr(), stream)
+            _lib.call("lm_moe_gate_up", z.data_ptr(), w["input_linear"].data_ptr(), None, None,
+                      ids.data_ptr(), batch * k, k, H, I, E, 0, act.data_ptr(), stream)
 
     def fused_all():
         for w, weights, ids, *_ in per_layer:

@@ -209,20 +209,25 @@ int lm_fused_experts(const void *x, const void *w13, const void *w2,
                      int64_t block_rows, void *out, void *workspace,
                      int64_t workspace_bytes, void *stream);
 
-/* Stage entry points of lm_fused_experts, exposed for parity tests.
- * gate_up: act[p, :] = bf16(silu(bf16(g)) * bf16(u)) for sorted position p,
- *   g/u = W13[e] . x[sorted_routes[p] / topk]; act is [routes, inter].
- * down: y[sorted_routes[p], :] = bf16(W2[e] . act[p, :]); y is [routes,
- *   hidden] in route order. Routes of the ignored tail are not touched. */
+/* Stage entry points of lm_fused_experts, exposed for parity tests and
+ * kernel timing. For a route r = t*topk + j of expert e:
+ * gate_up: act[r, :] = bf16(silu(bf16(g)) * bf16(u)),
+ *   g/u = W13[e] . x[r / topk]; act is [routes, inter] in route order.
+ * down: y[r, :] = bf16(W2[e] . act[r, :]); y is [routes, hidden] in route
+ *   order. Routes of the ignored tail are not touched.
+ * With topk_ids given (routes <= 2048, at most 256 routes per expert) each
+ * expert's workgroups collect
+ * its routes themselves and expert_offsets/sorted_routes may be NULL;
+ * otherwise the routes come from lm_moe_align's offsets and permutation. */
 int lm_moe_gate_up(const void *x, const void *w13,
                    const int32_t *expert_offsets, const int32_t *sorted_routes,
-                   int64_t routes, int64_t topk, int64_t hidden, int64_t inter,
-                   int64_t experts, int64_t block_rows, void *act,
-                   void *stream);
+                   const int32_t *topk_ids, int64_t routes, int64_t topk,
+                   int64_t hidden, int64_t inter, int64_t experts,
+                   int64_t block_rows, void *act, void *stream);
 int lm_moe_down(const void *act, const void *w2, const int32_t *expert_offsets,
-                const int32_t *sorted_routes, int64_t routes, int64_t hidden,
-                int64_t inter, int64_t experts, int64_t block_rows, void *y,
-                void *stream);
+                const int32_t *sorted_routes, const int32_t *topk_ids,
+                int64_t routes, int64_t hidden, int64_t inter, int64_t experts,
+                int64_t block_rows, void *y, void *stream);
 
 /* Weighted combine of route outputs, fp32 ordered accumulation:
  *   out[t,:] = bf16( sum over j in ascending (logical[ids[t,j]]*K + j) of
@@ -240,6 +245,56 @@ int lm_moe_finish(const void *y, const int32_t *ids, const int64_t *order,
                   int64_t tokens, int64_t hidden, int64_t topk, int64_t rank,
                   int64_t count, void *workspace, int64_t workspace_bytes,
                   void *stream);
+
+/* ------------------------------------------------------ fused decode ops -- */
+
+/* Residual add, RMSNorm and the router in one pass per token:
+ *   x[t] <- bf16(x[t] + alpha * a[t]);  z[t] = rmsnorm(x[t]) (lm_rmsnorm);
+ *   then lm_router on z[t] (logits_out may be NULL).
+ * a may be NULL (x only normalised). Fuses litemoe/model.py:108-113: the
+ * residual update, the post-attention norm, the router GEMV and vLLM
+ * fused_topk. Same limits as lm_router. */
+int lm_add_rmsnorm_router(void *x, const void *a, float alpha,
+                          const void *norm_weight, float eps, void *z,
+                          const void *gate_weight, int64_t tokens,
+                          int64_t hidden, int64_t experts, int64_t topk,
+                          int renormalize, void *logits_out,
+                          float *topk_weights, int32_t *topk_ids,
+                          void *stream);
+
+/* Workspace for lm_moe_routes. */
+int lm_moe_routes_workspace_size(int64_t tokens, int64_t topk, int64_t hidden,
+                                 int64_t inter, int64_t experts,
+                                 int64_t *bytes);
+
+/* Per-route expert outputs, unweighted, in route order r = t*topk + j:
+ *   y[r] = bf16(W2[e] . bf16(silu(bf16(W13[e,:I] x_t)) * bf16(W13[e,I:] x_t)))
+ * (the first half of lm_fused_experts; combine with lm_moe_finish or
+ * lm_moe_finish_add_rmsnorm). Decode-sized batches (tokens <= 256 and
+ * tokens * topk <= 2048) take a
+ * path where each expert's workgroups collect that expert's routes
+ * themselves (no permutation pass); larger batches use lm_moe_align blocks.
+ * Replaces the expert GEMMs inside vLLM fused_experts (litemoe/ep.py:40-41)
+ * and the per-expert loop of litemoe/ops.py:43-47. Shapes as
+ * lm_fused_experts; y: [tokens*topk, hidden] bf16. */
+int lm_moe_routes(const void *x, const void *w13, const void *w2,
+                  const int32_t *topk_ids, int64_t tokens, int64_t hidden,
+                  int64_t inter, int64_t experts, int64_t topk,
+                  int64_t block_rows, void *y, void *workspace,
+                  int64_t workspace_bytes, void *stream);
+
+/* The combine of lm_moe_finish (y in route order, all routes owned) fused
+ * with the residual add and the next RMSNorm:
+ *   m[t] = bf16(finish(y, ids, scales)[t]);  x[t] <- bf16(x[t] + alpha*m[t]);
+ *   z[t] = rmsnorm(x[t], norm_weight).
+ * Replaces moe_finish (litemoe/moe_finish.py:7-57) followed by
+ * litemoe/model.py:122 and the next layer's :106 (or the final norm :126).
+ * logical as lm_moe_finish (NULL = identity). */
+int lm_moe_finish_add_rmsnorm(const void *y, const int32_t *ids,
+                              const float *scales, const int64_t *logical,
+                              void *x, float alpha, const void *norm_weight,
+                              float eps, void *z, int64_t tokens,
+                              int64_t hidden, int64_t topk, void *stream);
 
 #ifdef __cplusplus
 }

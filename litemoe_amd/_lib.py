@@ -39,9 +39,13 @@ _SIGNATURES = {
     "lm_fused_experts_workspace_size": [_i64, _i64, _i64, _i64, _i64, C.POINTER(C.c_int64)],
     "lm_fused_experts": [_v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v,
                          _i64, _v],
-    "lm_moe_gate_up": [_v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v],
-    "lm_moe_down": [_v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _v, _v],
+    "lm_moe_gate_up": [_v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v],
+    "lm_moe_down": [_v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _v, _v],
     "lm_moe_finish": [_v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _v, _i64, _v],
+    "lm_add_rmsnorm_router": [_v, _v, _f32, _v, _f32, _v, _v, _i64, _i64, _i64, _i64, _i32, _v, _v, _v, _v],
+    "lm_moe_routes_workspace_size": [_i64, _i64, _i64, _i64, _i64, C.POINTER(C.c_int64)],
+    "lm_moe_routes": [_v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v, _i64, _v],
+    "lm_moe_finish_add_rmsnorm": [_v, _v, _v, _v, _v, _f32, _v, _f32, _v, _i64, _i64, _i64, _v],
 }
 _RESTYPE = {"lm_version": C.c_char_p, "lm_status_string": C.c_char_p}
 

@@ -2,13 +2,16 @@
 // [batch, kv_heads, capacity, 64] (one "page" per row, as the reference's
 // paged call uses block_table = arange(batch), litemoe/flash_decode.py:10-12).
 //
-// Workgroup (split, kv head, row) covers keys [split*chunk, (split+1)*chunk)
-// clipped to used[row]. Lane l owns key slot l/4 of each 16-key group and
-// channels 16*(l%4) .. +15; it keeps its own online-softmax state (max, sum,
-// 16-channel accumulator) for the G query heads of the kv head, so no
-// cross-lane reduction is needed inside the key loop except the 4-lane dot
-// product sum. States are merged by log-sum-exp across lanes, waves, and
-// (second kernel) splits.
+// Workgroup (split, kv head, row), 8 waves, covers keys
+// [split*chunk, (split+1)*chunk) clipped to used[row]. A wave takes 16
+// consecutive keys per iteration: lane l owns key slot l/8 of two 8-key
+// groups and channels 8*(l%8) .. +7 (one 16-byte load per key for K and for
+// V, 1 KB contiguous per wave load). The q.k dot product is summed over the 8
+// lanes of a key with DPP lane moves; each lane keeps an online-softmax state
+// (max, sum, 8-channel accumulator) per query head of the kv head, identical
+// across the 8 lanes of a key slot. The next iteration's K/V loads are in
+// flight while the current one is computed. States merge by log-sum-exp
+// across key slots, waves, and (second kernel, only when split) splits.
 //
 // Reference semantics: softmax(scale * q.K^T) V over keys j < seqused_k,
 // litemoe/flash_decode.py:16-22; masking litemoe/cache.py:42-47.
@@ -18,10 +21,13 @@ namespace lm {
 namespace {
 
 constexpr int kD = 64;
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kKeysPerWave = 16;   // 64 lanes / 4 lanes per key
-constexpr int kUnroll = 2;         // key groups in flight per lane
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kLanesPerKey = 8;
+constexpr int kSlots = kWave / kLanesPerKey;  // key slots per wave
+constexpr int kU = 2;                         // key groups per lane per iteration
+constexpr int kKeysPerWave = kSlots * kU;     // 16
+constexpr int kKeysPerIter = kKeysPerWave * kWaves;
 
 struct Partial {
   float *o;  // [batch, q_heads, splits, 64]
@@ -35,11 +41,10 @@ __device__ __forceinline__ float merge_factor(float m, float mnew) {
 
 template <int G>
 __global__ void __launch_bounds__(kThreads)
-decode_partial_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1,
-                      const bf16 *__restrict__ kc, const bf16 *__restrict__ vc,
-                      const int32_t *__restrict__ used, int q_heads, int kv_heads,
-                      int64_t capacity, float scale, int max_len, int chunk, int splits,
-                      Partial part, bf16 *__restrict__ out) {
+decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 *__restrict__ kc,
+              const bf16 *__restrict__ vc, const int32_t *__restrict__ used, int q_heads,
+              int kv_heads, int64_t capacity, float scale, int max_len, int chunk, int splits,
+              Partial part, bf16 *__restrict__ out) {
   __shared__ float sm_o[kWaves][G][kD];
   __shared__ float sm_m[kWaves][G];
   __shared__ float sm_l[kWaves][G];
@@ -52,87 +57,89 @@ decode_partial_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1,
   const int k1 = min(n, k0 + chunk);
   if (splits > 1 && k0 >= n) return;  // the combine kernel skips empty splits
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int ks = lane / 4, dc = lane % 4;
-  // q channels 16*dc .. +15 of the G heads, pre-scaled.
-  float qv[G][16];
+  const int ks = lane / kLanesPerKey, dc = lane % kLanesPerKey;
+  float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const bf16 *qp = q + b * qs0 + (int64_t)(h * G + g) * qs1 + dc * 16;
-    float f[8];
-    unpack8(*reinterpret_cast<const u32x4 *>(qp), f);
+    const bf16 *qp = q + b * qs0 + (int64_t)(h * G + g) * qs1 + dc * 8;
+    unpack8(*reinterpret_cast<const u32x4 *>(qp), qv[g]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qv[g][i] = f[i] * scale;
-    unpack8(*reinterpret_cast<const u32x4 *>(qp + 8), f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qv[g][8 + i] = f[i] * scale;
+    for (int i = 0; i < 8; ++i) qv[g][i] *= scale;
   }
-  float m[G], l[G], acc[G][16];
+  float m[G], l[G], acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
     l[g] = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[g][i] = 0.f;
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
   }
-  const int64_t head_base = ((int64_t)b * kv_heads + h) * capacity * kD + dc * 16;
+  const int64_t head_base = ((int64_t)b * kv_heads + h) * capacity * kD + dc * 8;
   const bf16 *kbase = kc + head_base;
   const bf16 *vbase = vc + head_base;
-  constexpr int kStep = kWaves * kKeysPerWave * kUnroll;
-  for (int j0 = k0 + wave * kKeysPerWave * kUnroll; j0 < k1; j0 += kStep) {
-    u32x4 kw[kUnroll][2], vw[kUnroll][2];
-    bool ok[kUnroll];
+  const int first = k0 + wave * kKeysPerWave + ks;  // key of group 0 in iteration 0
+  const int niter = k1 > k0 ? (k1 - k0 + kKeysPerIter - 1) / kKeysPerIter : 0;
+
+  auto load = [&](u32x4 *kb, u32x4 *vb, int it) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = j0 + u * kKeysPerWave + ks;
-      ok[u] = j < k1;
-      const int64_t off = (int64_t)(ok[u] ? j : k0) * kD;
-      kw[u][0] = *reinterpret_cast<const u32x4 *>(kbase + off);
-      kw[u][1] = *reinterpret_cast<const u32x4 *>(kbase + off + 8);
-      vw[u][0] = *reinterpret_cast<const u32x4 *>(vbase + off);
-      vw[u][1] = *reinterpret_cast<const u32x4 *>(vbase + off + 8);
+    for (int u = 0; u < kU; ++u) {
+      const int j = min(first + it * kKeysPerIter + u * kSlots, k1 - 1);
+      kb[u] = *reinterpret_cast<const u32x4 *>(kbase + (int64_t)j * kD);
+      vb[u] = *reinterpret_cast<const u32x4 *>(vbase + (int64_t)j * kD);
     }
-    float s[kUnroll][G];
+  };
+  auto compute = [&](const u32x4 *kb, const u32x4 *vb, int it) {
+    float s[kU][G];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float kf[16];
-      unpack8(kw[u][0], kf);
-      unpack8(kw[u][1], kf + 8);
+    for (int u = 0; u < kU; ++u) {
+      const bool ok = first + it * kKeysPerIter + u * kSlots < k1;
+      float kf[8];
+      unpack8(kb[u], kf);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float d = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) d = fmaf(qv[g][i], kf[i], d);
-        d += shfl_xor(d, 1);
-        d += shfl_xor(d, 2);
-        s[u][g] = ok[u] ? d : -INFINITY;
+        for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], kf[i], d);
+        d = dpp_sum8(d);
+        s[u][g] = ok ? d : -INFINITY;
       }
     }
+    float vf[kU][8];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) unpack8(vb[u], vf[u]);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float mx = m[g];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) mx = fmaxf(mx, s[u][g]);
+      for (int u = 0; u < kU; ++u) mx = fmaxf(mx, s[u][g]);
       if (mx == -INFINITY) continue;
       const float corr = merge_factor(m[g], mx);
       m[g] = mx;
       l[g] *= corr;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[g][i] *= corr;
+      for (int i = 0; i < 8; ++i) acc[g][i] *= corr;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const float p = __expf(s[u][g] - mx);
+      for (int u = 0; u < kU; ++u) {
+        const float p = s[u][g] == -INFINITY ? 0.f : __expf(s[u][g] - mx);
         l[g] += p;
-        float vf[16];
-        unpack8(vw[u][0], vf);
-        unpack8(vw[u][1], vf + 8);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
+        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[u][i], acc[g][i]);
       }
     }
+  };
+
+  u32x4 ka[kU], va[kU], kb2[kU], vb2[kU];
+  if (niter > 0) load(ka, va, 0);
+  for (int it = 0; it < niter; it += 2) {
+    if (it + 1 < niter) load(kb2, vb2, it + 1);
+    compute(ka, va, it);
+    if (it + 2 < niter) load(ka, va, it + 2);
+    if (it + 1 < niter) compute(kb2, vb2, it + 1);
   }
-  // Merge the 16 key slots of the wave (lanes with equal dc).
+
+  // Merge the 8 key slots of the wave (lanes with equal dc).
 #pragma unroll
-  for (int mask = 4; mask < kWave; mask <<= 1) {
+  for (int mask = kLanesPerKey; mask < kWave; mask <<= 1) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float mo = shfl_xor(m[g], mask);
@@ -141,7 +148,7 @@ decode_partial_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1,
       const float fa = merge_factor(m[g], mn), fb = merge_factor(mo, mn);
       l[g] = l[g] * fa + lo * fb;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[g][i] = acc[g][i] * fa + shfl_xor(acc[g][i], mask) * fb;
+      for (int i = 0; i < 8; ++i) acc[g][i] = acc[g][i] * fa + shfl_xor(acc[g][i], mask) * fb;
       m[g] = mn;
     }
   }
@@ -149,7 +156,7 @@ decode_partial_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1,
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sm_o[wave][g][dc * 16 + i] = acc[g][i];
+      for (int i = 0; i < 8; ++i) sm_o[wave][g][dc * 8 + i] = acc[g][i];
       if (dc == 0) {
         sm_m[wave][g] = m[g];
         sm_l[wave][g] = l[g];
@@ -255,12 +262,12 @@ extern "C" int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1, const vo
   hipStream_t s = (hipStream_t)stream;
   const int G = (int)(q_heads / kv_heads);
   switch (G) {
-#define X(GG)                                                                                    \
-  case GG:                                                                                       \
-    decode_partial_kernel<GG><<<grid, kThreads, 0, s>>>(                                         \
-        (const bf16 *)q, qs0, qs1, (const bf16 *)k_cache, (const bf16 *)v_cache, used,           \
-        (int)q_heads, (int)kv_heads, capacity, scale, (int)max_len, chunk, stride_splits, part,  \
-        (bf16 *)out);                                                                            \
+#define X(GG)                                                                                   \
+  case GG:                                                                                      \
+    decode_kernel<GG><<<grid, kThreads, 0, s>>>((const bf16 *)q, qs0, qs1, (const bf16 *)k_cache, \
+                                                 (const bf16 *)v_cache, used, (int)q_heads,       \
+                                                 (int)kv_heads, capacity, scale, (int)max_len,     \
+                                                 chunk, stride_splits, part, (bf16 *)out);         \
     break;
     X(1) X(2) X(3) X(4) X(6) X(8)
 #undef X

@@ -65,6 +65,16 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Sum over aligned groups of 8 lanes with DPP lane moves (no LDS crossbar):
+// quad_perm xor 1, quad_perm xor 2, then row_half_mirror (lane i <- 7-i).
+// Every lane of the group ends with the same, bitwise identical sum.
+__device__ __forceinline__ float dpp_sum8(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));
+  return v;
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
 // MFMA 16x16x32 bf16 (gfx950). Lane l supplies row l%16 of A and column l%16

@@ -11,13 +11,16 @@ int launch_finish(const bf16 *y, const int32_t *ids, const int32_t *inverse, con
                   const int64_t *logical, bf16 *out, int64_t tokens, int64_t hidden, int64_t topk,
                   int64_t rank, int64_t count, hipStream_t stream);
 
-// moe_gemm.hip
+// moe_gemm.hip. With ids != nullptr a launch takes the scan path (grid.y =
+// expert, routes collected from ids); otherwise offsets/sorted blocks.
 int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const int32_t *sorted,
-                   int64_t routes, int64_t topk, int64_t hidden, int64_t inter, int64_t experts,
-                   int64_t block_rows, bf16 *act, hipStream_t stream);
+                   const int32_t *ids, int64_t routes, int64_t topk, int64_t hidden, int64_t inter,
+                   int64_t experts, int64_t block_rows, bf16 *act, hipStream_t stream);
 int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const int32_t *sorted,
-                int64_t routes, int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
-                bf16 *y, hipStream_t stream);
+                const int32_t *ids, int64_t routes, int64_t hidden, int64_t inter, int64_t experts,
+                int64_t block_rows, bf16 *y, hipStream_t stream);
+bool expert_shapes_ok(int64_t hidden, int64_t inter);
+bool scan_path(int64_t tokens, int64_t topk);
 
 // Rows of one weight-tile block; 0 picks min(align16(tokens), 256).
 int pick_block_rows(int64_t block_rows, int64_t tokens);

@@ -72,6 +72,85 @@ finish_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ ids,
   }
 }
 
+// Finish fused with the residual add and the next RMSNorm; one workgroup per
+// token, 8 columns per thread, hidden <= kMaxVec * 8 * 256.
+constexpr int kMaxVec = 2;
+
+__global__ void __launch_bounds__(256)
+finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ ids,
+                       const float *__restrict__ scales, const int64_t *__restrict__ logical,
+                       bf16 *__restrict__ x, float alpha, const bf16 *__restrict__ w,
+                       float eps, bf16 *__restrict__ z, int hidden, int topk) {
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x;
+  int64_t key[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j) {
+    if (j < topk) {
+      const int64_t e = ids[t * topk + j];
+      key[j] = (logical ? logical[e] : e) * topk + j;
+    } else {
+      key[j] = INT64_MAX;
+    }
+  }
+  int order[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j) {
+    int r = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxK; ++i) r += key[i] < key[j];
+    order[j] = r;
+  }
+  const int nvec = hidden / 8;
+  float xn[kMaxVec][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < kMaxVec; ++v) {
+    const int i = threadIdx.x + v * 256;
+    if (i >= nvec) continue;
+    float total[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < topk; ++q) {
+      int sel = 0;
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j) sel += (order[j] == q) ? j : 0;
+      const int64_t r = t * topk + sel;
+      const float s = round_bf16(scales[r]);
+      float f[8];
+      unpack8(reinterpret_cast<const u32x4 *>(y + r * hidden)[i], f);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) total[c] += round_bf16(f[c] * s);
+    }
+    float xv[8];
+    unpack8(reinterpret_cast<const u32x4 *>(x + t * hidden)[i], xv);
+    u32x4 o;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      xn[v][c] = round_bf16(xv[c] + alpha * round_bf16(total[c]));
+      ss += xn[v][c] * xn[v][c];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = pack_bf16(xn[v][2 * c], xn[v][2 * c + 1]);
+    reinterpret_cast<u32x4 *>(x + t * hidden)[i] = o;
+  }
+  ss = wave_sum(ss);
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  const float scale = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)hidden + eps);
+#pragma unroll
+  for (int v = 0; v < kMaxVec; ++v) {
+    const int i = threadIdx.x + v * 256;
+    if (i >= nvec) continue;
+    float g[8];
+    unpack8(reinterpret_cast<const u32x4 *>(w)[i], g);
+    u32x4 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      o[c] = pack_bf16(round_bf16(xn[v][2 * c] * scale) * g[2 * c],
+                       round_bf16(xn[v][2 * c + 1] * scale) * g[2 * c + 1]);
+    reinterpret_cast<u32x4 *>(z + t * hidden)[i] = o;
+  }
+}
+
 __global__ void __launch_bounds__(256)
 invert_kernel(const int64_t *__restrict__ order, int64_t n, int32_t *__restrict__ inverse) {
   const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -122,4 +201,20 @@ extern "C" int lm_moe_finish(const void *y, const int32_t *ids, const int64_t *o
   }
   return launch_finish((const bf16 *)y, ids, inverse, scales, logical, (bf16 *)out, tokens, hidden,
                        topk, rank, count, s);
+}
+
+extern "C" int lm_moe_finish_add_rmsnorm(const void *y, const int32_t *ids, const float *scales,
+                                         const int64_t *logical, void *x, float alpha,
+                                         const void *norm_weight, float eps, void *z,
+                                         int64_t tokens, int64_t hidden, int64_t topk,
+                                         void *stream) {
+  LM_REQUIRE(tokens >= 0 && hidden > 0 && topk >= 1 && topk <= kMaxK);
+  if (hidden % 8 || hidden > kMaxVec * 8 * 256) return LM_EUNSUPPORTED;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(y && ids && scales && x && norm_weight && z);
+  finish_add_norm_kernel<<<dim3((unsigned)tokens), 256, 0, (hipStream_t)stream>>>(
+      (const bf16 *)y, ids, scales, logical, (bf16 *)x, alpha, (const bf16 *)norm_weight, eps,
+      (bf16 *)z, (int)hidden, (int)topk);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
 }

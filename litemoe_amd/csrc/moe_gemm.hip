@@ -1,19 +1,24 @@
 // Grouped SwiGLU expert GEMMs on MFMA (v_mfma_f32_16x16x32_bf16) for the
 // decode-sized MoE, where the expert weights are the HBM traffic:
 //
-//   gate_up: act[p] = bf16(silu(bf16(x_t . W13[e, j])) * bf16(x_t . W13[e, I+j]))
-//   down:    y[r]   = bf16(act[p] . W2[e, n])
+//   gate_up: act[r] = bf16(silu(bf16(x_t . W13[e, j])) * bf16(x_t . W13[e, I+j]))
+//   down:    y[r]   = bf16(act[r] . W2[e, n])
 //
-// for sorted position p of route r = sorted[p] (token t = r / topk) of expert
-// e. Workgroup (column tile, row block): 4 waves split the reduction dimension
-// K into quarters; each wave loads its slice of the workgroup's weight tile
-// into registers once, then streams the block's routes through it in 16-row
-// MFMA sub-blocks; the quarters are summed through LDS. A block is at most
-// block_rows routes of one expert, so each expert's weights are read once per
-// block (once per call when block_rows >= the route count of any expert).
-// Blocks are enumerated on the device from expert_offsets, so the grid is
-// fixed by the shapes alone (graph capture) and empty experts cost nothing
-// but an early exit.
+// for route r = t*topk + branch of expert e; act and y are in route order.
+// Workgroup = (column tile, route set of one expert). Its 4 waves split the
+// reduction dimension K into quarters; each wave loads its slice of the
+// workgroup's weight tile into registers once, then streams the route set
+// through it in 16-row MFMA sub-blocks; the quarters are summed through LDS.
+//
+// Two ways to find a workgroup's routes:
+//  * scan (decode, tokens <= kMaxScanRows): grid.y is the expert; the
+//    workgroup collects the expert's routes from topk_ids itself with one
+//    ballot per 64 routes, in ascending route order. No permutation pass.
+//  * blocks (prefill): lm_moe_align sorts routes by expert; grid.y enumerates
+//    blocks of at most block_rows routes of one expert, found on the device
+//    from expert_offsets. Each expert's weights are read once per block.
+// Both grids are fixed by the shapes alone (graph capture); an expert with
+// no routes costs an early exit.
 //
 // Reference: the expert math of litemoe/ops.py:43-47 (reference_experts) and
 // the vLLM fused_experts call at litemoe/ep.py:40-41.
@@ -24,6 +29,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxScanRows = 256;
 
 // Block b of the per-expert blocks of block_rows routes.
 __device__ __forceinline__ bool find_block(const int32_t *__restrict__ offsets, int experts, int bm,
@@ -44,34 +50,117 @@ __device__ __forceinline__ bool find_block(const int32_t *__restrict__ offsets, 
   return false;
 }
 
+// Route collection for the scan path, in two steps so that the ids loads
+// are issued before the weight loads (vector loads complete in issue order:
+// the scan then waits only for the ids, while the weights stream).
+// Wave w owns routes [w*seg, (w+1)*seg), seg a multiple of 64, at most
+// kScanIters loads of 64 ids per lane.
+constexpr int kScanIters = 8;  // routes <= kWaves * kScanIters * 64 = 2048
+
+struct ScanIds {
+  int id[kScanIters];
+  int begin;
+};
+
+__device__ __forceinline__ ScanIds load_ids(const int32_t *__restrict__ ids, int routes) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int seg = (int)(cdiv(cdiv(routes, kWaves), kWave) * kWave);
+  ScanIds s;
+  s.begin = wave * seg;
+  const int end = min(routes, s.begin + seg);
+#pragma unroll
+  for (int it = 0; it < kScanIters; ++it) {
+    const int r = s.begin + it * kWave + lane;
+    s.id[it] = r < end ? ids[r] : -1;
+  }
+  return s;
+}
+
+// Routes with id e, ascending, into list[]; returns the count. All threads
+// of the workgroup must call it (it synchronises).
+__device__ int scan_ids(const ScanIds &s, int e, int *list, int *wave_count) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const uint64_t below = (1ull << lane) - 1ull;
+  int count = 0;
+#pragma unroll
+  for (int it = 0; it < kScanIters; ++it) count += __popcll(__ballot(s.id[it] == e));
+  if (lane == 0) wave_count[wave] = count;
+  __syncthreads();
+  int offset = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    offset += w < wave ? wave_count[w] : 0;
+    total += wave_count[w];
+  }
+#pragma unroll
+  for (int it = 0; it < kScanIters; ++it) {
+    const bool hit = s.id[it] == e;
+    const uint64_t mask = __ballot(hit);
+    const int slot = offset + __popcll(mask & below);
+    if (hit && slot < kMaxScanRows) list[slot] = s.begin + it * kWave + lane;
+    offset += __popcll(mask);
+  }
+  __syncthreads();
+  return min(total, kMaxScanRows);  // a token picks an expert once: total <= tokens
+}
+
 __device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
-// KS: 32-wide k steps per wave, hidden = KS * 32 * kWaves.
-template <int KS>
+struct RouteSet {
+  const int32_t *sorted;  // blocks mode: route of sorted position p
+  const int *list;        // scan mode: LDS list of routes
+  int r0, r1;
+  __device__ __forceinline__ int route(int p) const { return list ? list[p] : sorted[p]; }
+};
+
+// KS: 32-wide k steps per wave, hidden = KS * 32 * kWaves. Column tile of 16
+// gate rows and the matching 16 up rows.
+template <int KS, bool kScan>
 __global__ void __launch_bounds__(kThreads)
 gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
-               const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted, int topk,
-               int hidden, int inter, int experts, int bm, bf16 *__restrict__ act) {
+               const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
+               const int32_t *__restrict__ ids, int routes, int topk, int hidden, int inter,
+               int experts, int bm, int prefetch, bf16 *__restrict__ act) {
   __shared__ float red[kWaves][2][4][kWave];
-  int e, r0, r1;
-  if (!find_block(offsets, experts, bm, blockIdx.y, e, r0, r1)) return;
+  __shared__ int list[kScan ? kMaxScanRows : 1];
+  __shared__ int wave_count[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
   const int n0 = blockIdx.x * 16;
   const int kbase = wave * KS * 32 + grp * 8;
-  const bf16 *wg = w13 + ((int64_t)e * 2 * inter + n0 + col) * hidden + kbase;
-  const bf16 *wu = wg + (int64_t)inter * hidden;
   u32x4 bg[KS], bu[KS];
+  auto load_weights = [&](int e) {
+    const bf16 *wg = w13 + ((int64_t)e * 2 * inter + n0 + col) * hidden + kbase;
+    const bf16 *wu = wg + (int64_t)inter * hidden;
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    bg[s] = load16(wg + s * 32);
-    bu[s] = load16(wu + s * 32);
+    for (int s = 0; s < KS; ++s) {
+      bg[s] = load16(wg + s * 32);
+      bu[s] = load16(wu + s * 32);
+    }
+  };
+  RouteSet set{sorted, nullptr, 0, 0};
+  if constexpr (kScan) {
+    const int e = blockIdx.y;
+    const ScanIds scan = load_ids(ids, routes);
+    __builtin_amdgcn_sched_barrier(0);  // keep the ids loads ahead of the weights
+    if (prefetch) load_weights(e);
+    __builtin_amdgcn_sched_barrier(0);
+    const int n = scan_ids(scan, e, list, wave_count);
+    if (n == 0) return;
+    if (!prefetch) load_weights(e);
+    set = RouteSet{nullptr, list, 0, n};
+  } else {
+    int e, r0, r1;
+    if (!find_block(offsets, experts, bm, blockIdx.y, e, r0, r1)) return;
+    load_weights(e);
+    set.r0 = r0;
+    set.r1 = r1;
   }
-  for (int rb = r0; rb < r1; rb += 16) {
+  for (int rb = set.r0; rb < set.r1; rb += 16) {
     const int p = rb + col;
     u32x4 a[KS];
-    if (p < r1) {
-      const bf16 *xr = x + (int64_t)(sorted[p] / topk) * hidden + kbase;
+    if (p < set.r1) {
+      const bf16 *xr = x + (int64_t)(set.route(p) / topk) * hidden + kbase;
 #pragma unroll
       for (int s = 0; s < KS; ++s) a[s] = load16(xr + s * 32);
     } else {
@@ -98,9 +187,9 @@ gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
       u += red[w][1][wave][lane];
     }
     const int row = rb + grp * 4 + wave;
-    if (row < r1) {
+    if (row < set.r1) {
       const float h = round_bf16(silu(round_bf16(g))) * round_bf16(u);
-      act[(int64_t)row * inter + n0 + col] = (bf16)f32_to_bf16(h);
+      act[(int64_t)set.route(row) * inter + n0 + col] = (bf16)f32_to_bf16(h);
     }
     __syncthreads();
   }
@@ -108,31 +197,52 @@ gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
 
 // KS: 32-wide k steps per wave, inter = KS * 32 * kWaves. Column tile of 32
 // (two MFMA tiles).
-template <int KS>
+template <int KS, bool kScan>
 __global__ void __launch_bounds__(kThreads)
 down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
-            const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted, int hidden,
-            int inter, int experts, int bm, bf16 *__restrict__ y) {
+            const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
+            const int32_t *__restrict__ ids, int routes, int hidden, int inter, int experts, int bm,
+            int prefetch, bf16 *__restrict__ y) {
   __shared__ float red[kWaves][2][4][kWave];
-  int e, r0, r1;
-  if (!find_block(offsets, experts, bm, blockIdx.y, e, r0, r1)) return;
+  __shared__ int list[kScan ? kMaxScanRows : 1];
+  __shared__ int wave_count[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
   const int n0 = blockIdx.x * 32;
   const int kbase = wave * KS * 32 + grp * 8;
-  const bf16 *w0 = w2 + ((int64_t)e * hidden + n0 + col) * inter + kbase;
-  const bf16 *w1 = w0 + (int64_t)16 * inter;
   u32x4 b0[KS], b1[KS];
+  auto load_weights = [&](int e) {
+    const bf16 *w0 = w2 + ((int64_t)e * hidden + n0 + col) * inter + kbase;
+    const bf16 *w1 = w0 + (int64_t)16 * inter;
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    b0[s] = load16(w0 + s * 32);
-    b1[s] = load16(w1 + s * 32);
+    for (int s = 0; s < KS; ++s) {
+      b0[s] = load16(w0 + s * 32);
+      b1[s] = load16(w1 + s * 32);
+    }
+  };
+  RouteSet set{sorted, nullptr, 0, 0};
+  if constexpr (kScan) {
+    const int e = blockIdx.y;
+    const ScanIds scan = load_ids(ids, routes);
+    __builtin_amdgcn_sched_barrier(0);  // keep the ids loads ahead of the weights
+    if (prefetch) load_weights(e);
+    __builtin_amdgcn_sched_barrier(0);
+    const int n = scan_ids(scan, e, list, wave_count);
+    if (n == 0) return;
+    if (!prefetch) load_weights(e);
+    set = RouteSet{nullptr, list, 0, n};
+  } else {
+    int e, r0, r1;
+    if (!find_block(offsets, experts, bm, blockIdx.y, e, r0, r1)) return;
+    load_weights(e);
+    set.r0 = r0;
+    set.r1 = r1;
   }
-  for (int rb = r0; rb < r1; rb += 16) {
+  for (int rb = set.r0; rb < set.r1; rb += 16) {
     const int p = rb + col;
     u32x4 a[KS];
-    if (p < r1) {
-      const bf16 *ar = act + (int64_t)p * inter + kbase;
+    if (p < set.r1) {
+      const bf16 *ar = act + (int64_t)set.route(p) * inter + kbase;
 #pragma unroll
       for (int s = 0; s < KS; ++s) a[s] = load16(ar + s * 32);
     } else {
@@ -158,8 +268,8 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
       v1 += red[w][1][wave][lane];
     }
     const int row = rb + grp * 4 + wave;
-    if (row < r1) {
-      bf16 *yr = y + (int64_t)sorted[row] * hidden + n0 + col;
+    if (row < set.r1) {
+      bf16 *yr = y + (int64_t)set.route(row) * hidden + n0 + col;
       yr[0] = (bf16)f32_to_bf16(v0);
       yr[16] = (bf16)f32_to_bf16(v1);
     }
@@ -170,7 +280,25 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
 // Supported k steps per wave (reduction length / 128).
 #define LM_KS_LIST(X) X(1) X(2) X(3) X(4) X(6) X(8) X(12) X(16)
 
+bool ks_ok(int64_t n) {
+  if (n % 128) return false;
+  switch (n / 128) {
+#define X(KS) case KS:
+    LM_KS_LIST(X)
+#undef X
+    return true;
+    default:
+      return false;
+  }
+}
+
+// Weight tiles are prefetched before the route scan when an empty expert is
+// unlikely (>= 4 routes per expert on average).
+int prefetch_flag(int64_t routes, int64_t experts) { return routes >= 4 * experts; }
+
 }  // namespace
+
+bool expert_shapes_ok(int64_t hidden, int64_t inter) { return ks_ok(hidden) && ks_ok(inter); }
 
 int pick_block_rows(int64_t block_rows, int64_t tokens) {
   if (block_rows > 0) return (int)block_rows;
@@ -180,19 +308,29 @@ int pick_block_rows(int64_t block_rows, int64_t tokens) {
   return (int)(bm > 256 ? 256 : (bm < 16 ? 16 : bm));
 }
 
+bool scan_path(int64_t tokens, int64_t topk) {
+  return tokens <= kMaxScanRows && tokens * topk <= kWaves * kScanIters * kWave;
+}
+
 int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const int32_t *sorted,
-                   int64_t routes, int64_t topk, int64_t hidden, int64_t inter, int64_t experts,
-                   int64_t block_rows, bf16 *act, hipStream_t stream) {
+                   const int32_t *ids, int64_t routes, int64_t topk, int64_t hidden, int64_t inter,
+                   int64_t experts, int64_t block_rows, bf16 *act, hipStream_t stream) {
   if (routes == 0) return LM_OK;
+  const bool scan = ids != nullptr;
   const int bm = (int)block_rows;
-  if (cdiv(routes, bm) + experts > 65535) return LM_EUNSUPPORTED;
-  const dim3 grid((unsigned)(inter / 16), (unsigned)(cdiv(routes, bm) + experts));
+  const int64_t gy = scan ? experts : cdiv(routes, bm) + experts;
+  if (gy > 65535) return LM_EUNSUPPORTED;
+  const dim3 grid((unsigned)(inter / 16), (unsigned)gy);
+  const int pf = prefetch_flag(routes, experts);
   switch (hidden / 128) {
-#define X(KS)                                                                                 \
-  case KS:                                                                                    \
-    gate_up_kernel<KS><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, (int)topk,     \
-                                                       (int)hidden, (int)inter, (int)experts, \
-                                                       bm, act);                              \
+#define X(KS)                                                                                   \
+  case KS:                                                                                      \
+    if (scan)                                                                                   \
+      gate_up_kernel<KS, true><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, ids,     \
+          (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, pf, act);          \
+    else                                                                                        \
+      gate_up_kernel<KS, false><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, ids,    \
+          (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, pf, act);          \
     break;
     LM_KS_LIST(X)
 #undef X
@@ -204,17 +342,24 @@ int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const
 }
 
 int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const int32_t *sorted,
-                int64_t routes, int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
-                bf16 *y, hipStream_t stream) {
+                const int32_t *ids, int64_t routes, int64_t hidden, int64_t inter, int64_t experts,
+                int64_t block_rows, bf16 *y, hipStream_t stream) {
   if (routes == 0) return LM_OK;
+  const bool scan = ids != nullptr;
   const int bm = (int)block_rows;
-  if (cdiv(routes, bm) + experts > 65535) return LM_EUNSUPPORTED;
-  const dim3 grid((unsigned)(hidden / 32), (unsigned)(cdiv(routes, bm) + experts));
+  const int64_t gy = scan ? experts : cdiv(routes, bm) + experts;
+  if (gy > 65535) return LM_EUNSUPPORTED;
+  const dim3 grid((unsigned)(hidden / 32), (unsigned)gy);
+  const int pf = prefetch_flag(routes, experts);
   switch (inter / 128) {
-#define X(KS)                                                                              \
-  case KS:                                                                                 \
-    down_kernel<KS><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, (int)hidden,  \
-                                                    (int)inter, (int)experts, bm, y);      \
+#define X(KS)                                                                                  \
+  case KS:                                                                                     \
+    if (scan)                                                                                  \
+      down_kernel<KS, true><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids,      \
+          (int)routes, (int)hidden, (int)inter, (int)experts, bm, pf, y);                      \
+    else                                                                                       \
+      down_kernel<KS, false><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids,     \
+          (int)routes, (int)hidden, (int)inter, (int)experts, bm, pf, y);                      \
     break;
     LM_KS_LIST(X)
 #undef X
@@ -230,25 +375,16 @@ int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const i
 using namespace lm;
 
 namespace {
-bool expert_shapes_ok(int64_t hidden, int64_t inter) {
-  auto ks_ok = [](int64_t n) {
-    if (n % 128) return false;
-    switch (n / 128) {
-      case 1: case 2: case 3: case 4: case 6: case 8: case 12: case 16: return true;
-      default: return false;
-    }
-  };
-  return ks_ok(hidden) && ks_ok(inter);
-}
-
 struct ExpertWorkspace {
   int32_t *offsets, *sorted;
   bf16 *act, *y;
   int64_t bytes;
 };
 
+// Layout: offsets [E+1], sorted [R] (block path only), act [R, I], and (for
+// lm_fused_experts) y [R, H].
 ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, int64_t inter,
-                      int64_t experts) {
+                      int64_t experts, bool with_y) {
   const int64_t routes = tokens * topk;
   char *p = static_cast<char *>(base);
   ExpertWorkspace w;
@@ -259,70 +395,108 @@ ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, 
   off += align_up(4 * routes, 256);
   w.act = reinterpret_cast<bf16 *>(p + off);
   off += align_up(2 * routes * inter, 256);
-  w.y = reinterpret_cast<bf16 *>(p + off);
-  off += align_up(2 * routes * hidden, 256);
+  w.y = with_y ? reinterpret_cast<bf16 *>(p + off) : nullptr;
+  if (with_y) off += align_up(2 * routes * hidden, 256);
   w.bytes = off;
   return w;
+}
+
+// act and y in route order.
+int run_routes(const void *x, const void *w13, const void *w2, const int32_t *topk_ids,
+               int64_t tokens, int64_t hidden, int64_t inter, int64_t experts, int64_t topk,
+               int64_t block_rows, bf16 *y, const ExpertWorkspace &w, void *stream) {
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t routes = tokens * topk;
+  if (scan_path(tokens, topk) && block_rows == 0) {
+    int rc = launch_gate_up((const bf16 *)x, (const bf16 *)w13, nullptr, nullptr, topk_ids, routes,
+                            topk, hidden, inter, experts, 0, w.act, s);
+    if (rc) return rc;
+    return launch_down(w.act, (const bf16 *)w2, nullptr, nullptr, topk_ids, routes, hidden, inter,
+                       experts, 0, y, s);
+  }
+  const int bm = pick_block_rows(block_rows, tokens);
+  int rc = lm_moe_align(topk_ids, routes, 0, experts, w.offsets, w.sorted, nullptr, stream);
+  if (rc) return rc;
+  rc = launch_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, nullptr, routes,
+                      topk, hidden, inter, experts, bm, w.act, s);
+  if (rc) return rc;
+  return launch_down(w.act, (const bf16 *)w2, w.offsets, w.sorted, nullptr, routes, hidden, inter,
+                     experts, bm, y, s);
 }
 }  // namespace
 
 extern "C" int lm_fused_experts_workspace_size(int64_t tokens, int64_t topk, int64_t hidden,
                                                int64_t inter, int64_t experts, int64_t *bytes) {
   LM_REQUIRE(bytes && tokens >= 0 && topk > 0 && hidden > 0 && inter > 0 && experts > 0);
-  *bytes = carve(nullptr, tokens, topk, hidden, inter, experts).bytes;
+  *bytes = carve(nullptr, tokens, topk, hidden, inter, experts, true).bytes;
+  return LM_OK;
+}
+
+extern "C" int lm_moe_routes_workspace_size(int64_t tokens, int64_t topk, int64_t hidden,
+                                            int64_t inter, int64_t experts, int64_t *bytes) {
+  LM_REQUIRE(bytes && tokens >= 0 && topk > 0 && hidden > 0 && inter > 0 && experts > 0);
+  *bytes = carve(nullptr, tokens, topk, hidden, inter, experts, false).bytes;
   return LM_OK;
 }
 
 extern "C" int lm_moe_gate_up(const void *x, const void *w13, const int32_t *expert_offsets,
-                              const int32_t *sorted_routes, int64_t routes, int64_t topk,
-                              int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
-                              void *act, void *stream) {
+                              const int32_t *sorted_routes, const int32_t *topk_ids, int64_t routes,
+                              int64_t topk, int64_t hidden, int64_t inter, int64_t experts,
+                              int64_t block_rows, void *act, void *stream) {
   LM_REQUIRE(routes >= 0 && topk > 0 && experts > 0 && block_rows >= 0 && block_rows % 16 == 0);
   if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
+  if (topk_ids && !scan_path(routes / topk, topk)) return LM_EUNSUPPORTED;
   if (routes == 0) return LM_OK;
-  LM_REQUIRE(x && w13 && expert_offsets && sorted_routes && act);
-  return launch_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets, sorted_routes, routes,
-                        topk, hidden, inter, experts, pick_block_rows(block_rows, routes),
+  LM_REQUIRE(x && w13 && act && (topk_ids || (expert_offsets && sorted_routes)));
+  return launch_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets, sorted_routes, topk_ids,
+                        routes, topk, hidden, inter, experts, pick_block_rows(block_rows, routes),
                         (bf16 *)act, (hipStream_t)stream);
 }
 
 extern "C" int lm_moe_down(const void *act, const void *w2, const int32_t *expert_offsets,
-                           const int32_t *sorted_routes, int64_t routes, int64_t hidden,
-                           int64_t inter, int64_t experts, int64_t block_rows, void *y,
-                           void *stream) {
+                           const int32_t *sorted_routes, const int32_t *topk_ids, int64_t routes,
+                           int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
+                           void *y, void *stream) {
   LM_REQUIRE(routes >= 0 && experts > 0 && block_rows >= 0 && block_rows % 16 == 0);
   if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
+  if (topk_ids && routes > kWaves * kScanIters * kWave) return LM_EUNSUPPORTED;
   if (routes == 0) return LM_OK;
-  LM_REQUIRE(act && w2 && expert_offsets && sorted_routes && y);
-  return launch_down((const bf16 *)act, (const bf16 *)w2, expert_offsets, sorted_routes, routes,
-                     hidden, inter, experts, pick_block_rows(block_rows, routes), (bf16 *)y,
+  LM_REQUIRE(act && w2 && y && (topk_ids || (expert_offsets && sorted_routes)));
+  return launch_down((const bf16 *)act, (const bf16 *)w2, expert_offsets, sorted_routes, topk_ids,
+                     routes, hidden, inter, experts, pick_block_rows(block_rows, routes), (bf16 *)y,
                      (hipStream_t)stream);
+}
+
+extern "C" int lm_moe_routes(const void *x, const void *w13, const void *w2,
+                             const int32_t *topk_ids, int64_t tokens, int64_t hidden,
+                             int64_t inter, int64_t experts, int64_t topk, int64_t block_rows,
+                             void *y, void *workspace, int64_t workspace_bytes, void *stream) {
+  LM_REQUIRE(tokens >= 0 && topk > 0 && topk <= experts && block_rows >= 0 &&
+             block_rows % 16 == 0 && experts <= 511);
+  if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(x && w13 && w2 && topk_ids && y && workspace);
+  ExpertWorkspace w = carve(workspace, tokens, topk, hidden, inter, experts, false);
+  if (workspace_bytes < w.bytes) return LM_EWORKSPACE;
+  return run_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows,
+                    (bf16 *)y, w, stream);
 }
 
 extern "C" int lm_fused_experts(const void *x, const void *w13, const void *w2,
                                 const float *topk_weights, const int32_t *topk_ids,
                                 const int64_t *logical, int64_t tokens, int64_t hidden,
-                                int64_t inter, int64_t experts,
-                                int64_t topk, int64_t block_rows, void *out, void *workspace,
-                                int64_t workspace_bytes, void *stream) {
+                                int64_t inter, int64_t experts, int64_t topk, int64_t block_rows,
+                                void *out, void *workspace, int64_t workspace_bytes, void *stream) {
   LM_REQUIRE(tokens >= 0 && topk > 0 && topk <= 8 && topk <= experts && block_rows >= 0 &&
-             block_rows % 16 == 0);
+             block_rows % 16 == 0 && experts <= 511);
   if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(x && w13 && w2 && topk_weights && topk_ids && out && workspace);
-  ExpertWorkspace w = carve(workspace, tokens, topk, hidden, inter, experts);
+  ExpertWorkspace w = carve(workspace, tokens, topk, hidden, inter, experts, true);
   if (workspace_bytes < w.bytes) return LM_EWORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
-  const int64_t routes = tokens * topk;
-  const int bm = pick_block_rows(block_rows, tokens);
-  int rc = lm_moe_align(topk_ids, routes, 0, experts, w.offsets, w.sorted, nullptr, stream);
-  if (rc) return rc;
-  rc = launch_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, routes, topk,
-                      hidden, inter, experts, bm, w.act, s);
-  if (rc) return rc;
-  rc = launch_down(w.act, (const bf16 *)w2, w.offsets, w.sorted, routes, hidden, inter, experts,
-                   bm, w.y, s);
+  int rc = run_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows, w.y,
+                      w, stream);
   if (rc) return rc;
   return launch_finish(w.y, topk_ids, nullptr, topk_weights, logical, (bf16 *)out, tokens, hidden,
-                       topk, 0, experts, s);
+                       topk, 0, experts, (hipStream_t)stream);
 }

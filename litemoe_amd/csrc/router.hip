@@ -122,6 +122,99 @@ topk_from_logits_kernel(const bf16 *__restrict__ logits, int experts, int topk, 
   select_topk(logit, experts, topk, renormalize, tw + row * topk, tid + row * topk);
 }
 
+// Residual add + RMSNorm + router GEMV + top-k, one workgroup per token.
+// The normalised row stays in LDS for the GEMV; wave w computes the logits of
+// experts w, w+4, ... two at a time.
+constexpr int kMaxNormVec = 2;  // hidden <= kMaxNormVec * 8 * kRouterThreads
+
+__global__ void __launch_bounds__(kRouterThreads)
+add_norm_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha,
+                       const bf16 *__restrict__ nw, float eps, bf16 *__restrict__ z,
+                       const bf16 *__restrict__ wr, int hidden, int experts, int topk,
+                       int renormalize, bf16 *__restrict__ logits_out, float *__restrict__ tw,
+                       int32_t *__restrict__ tid) {
+  __shared__ u32x4 zs[kMaxNormVec * kRouterThreads];
+  __shared__ float logit[kMaxExperts];
+  __shared__ float red[kRouterThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int nvec = hidden / 8;
+  u32x4 *xr = reinterpret_cast<u32x4 *>(x + row * hidden);
+  float xn[kMaxNormVec][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < kMaxNormVec; ++v) {
+    const int i = threadIdx.x + v * kRouterThreads;
+    if (i >= nvec) continue;
+    unpack8(xr[i], xn[v]);
+    if (a) {
+      float g[8];
+      unpack8(reinterpret_cast<const u32x4 *>(a + row * hidden)[i], g);
+      u32x4 o;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) xn[v][c] = round_bf16(xn[v][c] + alpha * g[c]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = pack_bf16(xn[v][2 * c], xn[v][2 * c + 1]);
+      xr[i] = o;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ss += xn[v][c] * xn[v][c];
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRouterThreads / kWave; ++w) total += red[w];
+  const float scale = 1.0f / sqrtf(total / (float)hidden + eps);
+#pragma unroll
+  for (int v = 0; v < kMaxNormVec; ++v) {
+    const int i = threadIdx.x + v * kRouterThreads;
+    if (i >= nvec) continue;
+    float g[8];
+    unpack8(reinterpret_cast<const u32x4 *>(nw)[i], g);
+    u32x4 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      o[c] = pack_bf16(round_bf16(xn[v][2 * c] * scale) * g[2 * c],
+                       round_bf16(xn[v][2 * c + 1] * scale) * g[2 * c + 1]);
+    zs[i] = o;
+    reinterpret_cast<u32x4 *>(z + row * hidden)[i] = o;
+  }
+  __syncthreads();
+  for (int e0 = wave; e0 < experts; e0 += 2 * (kRouterThreads / kWave)) {
+    const int e1 = e0 + kRouterThreads / kWave;
+    const bool two = e1 < experts;
+    const u32x4 *w0 = reinterpret_cast<const u32x4 *>(wr + (int64_t)e0 * hidden);
+    const u32x4 *w1 = reinterpret_cast<const u32x4 *>(wr + (int64_t)(two ? e1 : e0) * hidden);
+    float acc0 = 0.f, acc1 = 0.f;
+    for (int i = lane; i < nvec; i += kWave) {
+      float zf[8], b0[8], b1[8];
+      unpack8(zs[i], zf);
+      unpack8(w0[i], b0);
+      unpack8(w1[i], b1);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        acc0 = fmaf(zf[c], b0[c], acc0);
+        acc1 = fmaf(zf[c], b1[c], acc1);
+      }
+    }
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    if (lane == 0) {
+      const uint32_t h0 = f32_to_bf16(acc0), h1 = f32_to_bf16(acc1);
+      logit[e0] = bf16_to_f32(h0);
+      if (logits_out) logits_out[row * experts + e0] = (bf16)h0;
+      if (two) {
+        logit[e1] = bf16_to_f32(h1);
+        if (logits_out) logits_out[row * experts + e1] = (bf16)h1;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) select_topk(logit, experts, topk, renormalize, tw + row * topk, tid + row * topk);
+}
+
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / kWave;
 constexpr int kMaxAlignExperts = 511;
@@ -233,6 +326,25 @@ extern "C" int lm_router(const void *x, const void *gate_weight, int64_t tokens,
   router_kernel<<<dim3((unsigned)tokens), kRouterThreads, 0, (hipStream_t)stream>>>(
       (const bf16 *)x, (const bf16 *)gate_weight, (int)hidden, (int)experts, (int)topk,
       renormalize, (bf16 *)logits_out, topk_weights, topk_ids);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+extern "C" int lm_add_rmsnorm_router(void *x, const void *a, float alpha, const void *norm_weight,
+                                     float eps, void *z, const void *gate_weight, int64_t tokens,
+                                     int64_t hidden, int64_t experts, int64_t topk, int renormalize,
+                                     void *logits_out, float *topk_weights, int32_t *topk_ids,
+                                     void *stream) {
+  LM_REQUIRE(tokens >= 0 && hidden > 0 && experts > 0 && topk > 0);
+  if (hidden % 8 || hidden > kMaxNormVec * 8 * kRouterThreads || experts > kMaxExperts ||
+      topk > kMaxTopk || topk > experts)
+    return LM_EUNSUPPORTED;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(x && norm_weight && z && gate_weight && topk_weights && topk_ids);
+  add_norm_router_kernel<<<dim3((unsigned)tokens), kRouterThreads, 0, (hipStream_t)stream>>>(
+      (bf16 *)x, (const bf16 *)a, alpha, (const bf16 *)norm_weight, eps, (bf16 *)z,
+      (const bf16 *)gate_weight, (int)hidden, (int)experts, (int)topk, renormalize,
+      (bf16 *)logits_out, topk_weights, topk_ids);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

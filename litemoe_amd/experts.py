@@ -83,6 +83,10 @@ class HipFusedExperts:
                              global_num_experts, out=out, block_rows=self.block_rows,
                              workspace=self.workspace)
 
+    def routes(self, x, w1, w2, topk_ids):
+        """Unweighted per-route expert outputs ``[M*k, H]`` in route order."""
+        return moe_routes(x, w1, w2, topk_ids, block_rows=self.block_rows, workspace=self.workspace)
+
     def __call__(self, x, ids, scales, w1, w2, rank, world, out, logical=None):
         if rank != 0 or world != 1:
             raise ValueError('The fused-expert backend supports EP1 only')
@@ -90,6 +94,42 @@ class HipFusedExperts:
             raise ValueError('Contiguous CUDA BF16 activations/weights/output required')
         return fused_experts(x, w1, w2, scales.float(), ids.int(), out=out, logical=logical,
                              block_rows=self.block_rows, workspace=self.workspace)
+
+
+def moe_routes(x, w1, w2, topk_ids, block_rows=0, workspace=None, y=None):
+    """``y[t*k + j] = W2[e] (silu(W13[e,:I] x_t) * W13[e,I:] x_t)`` (bf16
+    roundings as lm_fused_experts), unweighted, in route order."""
+    experts, hidden, inter = _check_weights(x, w1, w2)
+    tokens = x.numel() // hidden
+    ids = topk_ids.to(torch.int32).contiguous()
+    topk = ids.shape[-1]
+    if ids.shape[0] != tokens:
+        raise ValueError('Router outputs must be [tokens, topk]')
+    y = torch.empty(tokens * topk, hidden, device=x.device, dtype=x.dtype) if y is None else y
+    nbytes = _lib.size_query("lm_moe_routes_workspace_size", tokens, topk, hidden, inter, experts)
+    ws = (workspace or _SHARED).get(x.device, nbytes)
+    _lib.call("lm_moe_routes", x.data_ptr(), w1.data_ptr(), w2.data_ptr(), ids.data_ptr(), tokens, hidden,
+              inter, experts, topk, block_rows, y.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(x.device))
+    return y
+
+
+def finish_add_rmsnorm(y, ids, scales, x, alpha, norm_weight, eps, z=None, logical=None):
+    """Combine route outputs (moe_finish order and rounding), then
+    ``x <- bf16(x + alpha * out)`` and ``z = rmsnorm(x)`` in one kernel."""
+    _lib.require_cuda(y, ids, scales, x, norm_weight, what="combine inputs")
+    tokens, hidden = x.shape
+    topk = ids.shape[-1]
+    if y.shape != (tokens * topk, hidden) or scales.shape != ids.shape or not y.is_contiguous():
+        raise ValueError('Route outputs must be [tokens*topk, hidden] with [tokens, topk] ids/scales')
+    z = torch.empty_like(x) if z is None else z
+    ids32 = ids.to(torch.int32).contiguous()
+    w32 = scales.to(torch.float32).contiguous()
+    remap = logical is not None and logical.numel() != 0
+    logical64 = logical.to(torch.int64).contiguous() if remap else None
+    _lib.call("lm_moe_finish_add_rmsnorm", y.data_ptr(), ids32.data_ptr(), w32.data_ptr(), _lib.ptr(logical64),
+              x.data_ptr(), float(alpha), norm_weight.data_ptr(), float(eps), z.data_ptr(), tokens, hidden,
+              topk, _lib.stream(x.device))
+    return z
 
 
 def moe_align(topk_ids, local_experts, first_expert=0, inverse=True):
@@ -110,22 +150,26 @@ def moe_align(topk_ids, local_experts, first_expert=0, inverse=True):
     return offsets, order, inv
 
 
-def gate_up(x, w1, offsets, sorted_routes, topk, block_rows=0):
-    """Stage 1: ``act[p] = bf16(silu(bf16(g)) * bf16(u))`` per sorted route."""
-    experts, hidden, inter = _check_weights(x, w1, torch.empty(w1.shape[0], w1.shape[2], w1.shape[1] // 2,
-                                                              device=x.device, dtype=x.dtype))
-    routes = sorted_routes.numel()
-    act = torch.zeros(routes, inter, device=x.device, dtype=x.dtype)
-    _lib.call("lm_moe_gate_up", x.data_ptr(), w1.data_ptr(), offsets.data_ptr(), sorted_routes.data_ptr(),
-              routes, topk, hidden, inter, experts, block_rows, act.data_ptr(), _lib.stream(x.device))
+def gate_up(x, w1, offsets, sorted_routes, topk, block_rows=0, topk_ids=None, act=None):
+    """Stage 1: ``act[r] = bf16(silu(bf16(g)) * bf16(u))`` per route (route
+    order). Routes from ``lm_moe_align`` (offsets, sorted_routes) or, with
+    ``topk_ids``, collected by each expert's workgroups (decode path)."""
+    experts, two_inter, hidden = w1.shape
+    inter = two_inter // 2
+    routes = topk_ids.numel() if topk_ids is not None else sorted_routes.numel()
+    act = torch.zeros(routes, inter, device=x.device, dtype=x.dtype) if act is None else act
+    _lib.call("lm_moe_gate_up", x.data_ptr(), w1.data_ptr(), _lib.ptr(offsets), _lib.ptr(sorted_routes),
+              _lib.ptr(topk_ids), routes, topk, hidden, inter, experts, block_rows, act.data_ptr(),
+              _lib.stream(x.device))
     return act
 
 
-def down(act, w2, offsets, sorted_routes, block_rows=0):
-    """Stage 2: ``y[sorted[p]] = bf16(W2[e] . act[p])`` in route order."""
+def down(act, w2, offsets, sorted_routes, block_rows=0, topk_ids=None, y=None):
+    """Stage 2: ``y[r] = bf16(W2[e] . act[r])`` in route order."""
     experts, hidden, inter = w2.shape
-    routes = sorted_routes.numel()
-    y = torch.zeros(routes, hidden, device=act.device, dtype=act.dtype)
-    _lib.call("lm_moe_down", act.data_ptr(), w2.data_ptr(), offsets.data_ptr(), sorted_routes.data_ptr(),
-              routes, hidden, inter, experts, block_rows, y.data_ptr(), _lib.stream(act.device))
+    routes = topk_ids.numel() if topk_ids is not None else sorted_routes.numel()
+    y = torch.zeros(routes, hidden, device=act.device, dtype=act.dtype) if y is None else y
+    _lib.call("lm_moe_down", act.data_ptr(), w2.data_ptr(), _lib.ptr(offsets), _lib.ptr(sorted_routes),
+              _lib.ptr(topk_ids), routes, hidden, inter, experts, block_rows, y.data_ptr(),
+              _lib.stream(act.device))
     return y

@@ -13,9 +13,12 @@ import torch
 from . import _lib
 
 
-def default_splits(batch, kv_heads, maximum, keys_per_split=256, max_splits=16):
-    """Enough splits to fill the GPU at short contexts, chunks of ~256 keys."""
-    return max(1, min(max_splits, math.ceil(maximum / keys_per_split)))
+def default_splits(batch, kv_heads, maximum, target_workgroups=512, min_keys=256, max_splits=16):
+    """Split the key range only as far as needed to give the GPU about
+    ``target_workgroups`` (batch * kv_heads * splits) workgroups, keeping at
+    least ``min_keys`` keys per split; one split needs no combine pass."""
+    want = math.ceil(target_workgroups / max(1, batch * kv_heads))
+    return max(1, min(max_splits, want, maximum // min_keys))
 
 
 class FlashDecode:

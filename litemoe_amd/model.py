@@ -13,9 +13,13 @@ signature and tensor layouts. Per layer (decode and packed prefill alike):
     w, ids = router(z)                       lm_router (GEMV + top-k + softmax)
     y = experts(z, ids, w)                   lm_fused_experts (align, gate_up, down, finish)
 
-then ``x += r * y; logits = rmsnorm(x) . head^T / logits_scaling``. Dense
-projections stay on the vendor BLAS for now; every other step is a
-hand-written kernel. There is no CPU path: inputs must be on the GPU.
+then ``x += r * y; logits = rmsnorm(x) . head^T / logits_scaling``. With
+the library's experts, identity placement and no masked rows (lean decode,
+packed prefill) the layer tail is fused further into three launches:
+``lm_add_rmsnorm_router`` (x += r*a, norm, router), ``lm_moe_routes`` (expert
+GEMMs, route order) and ``lm_moe_finish_add_rmsnorm`` (combine, x += r*y,
+next layer's norm). Dense projections stay on the vendor BLAS for now; every
+other step is a hand-written kernel. There is no CPU path.
 """
 import torch
 import torch.nn.functional as F
@@ -23,9 +27,11 @@ import torch.nn.functional as F
 from . import _lib
 from .config import validate_config
 from .flash_decode import FlashDecode
+from .experts import finish_add_rmsnorm
 from .norm import add_rmsnorm
 from .packed import PackedPrefill, varlen_attention
 from .rope import rope_kv_write
+from .router import add_rmsnorm_route as route_add_rmsnorm
 from .router import route
 
 
@@ -87,6 +93,13 @@ class Granite:
                       cfg.attention_multiplier, self.used)
         return F.linear(a.reshape(rows, hq * d), w["self_attn.o_proj"])
 
+    def _fused_moe(self):
+        """The fused layer tail (add+norm+router, route GEMMs, combine+add+norm)
+        applies when the experts run on this library with identity placement
+        and no row needs masking (lean decode or packed prefill)."""
+        return getattr(self.ep.backend, "native", False) and all(
+            w["logical"].numel() == 0 for w in self.w["layers"])
+
     def forward(self, tokens, positions, valid, cache, slot=None, last=None, communication_tokens=None):
         cfg = self.cfg
         packed = isinstance(slot, PackedPrefill)
@@ -111,22 +124,34 @@ class Granite:
         masked = not packed and not self.decode_lean
         x = (F.embedding(tokens, self.w["embedding"]) * cfg.embedding_multiplier).reshape(b * s, hidden)
         x = x.contiguous()
-        z = torch.empty_like(x)
-        y = None
-        for layer, w in enumerate(self.w["layers"]):
-            add_rmsnorm(x, y, r, w["input_layernorm"], eps, out=z)
-            a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
-            if masked:
-                a = a * valid_rows[:, None]
-            add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps, out=z)
-            scales, ids = route(z, w["block_sparse_moe.router.layer"], cfg.num_experts_per_tok)
-            y = self.ep(z, ids, scales, valid_rows, w["physical"], w["input_linear"], w["output_linear"],
-                        w["logical"], decode=True, tokens=communication_tokens)
+        layers = self.w["layers"]
+        z = add_rmsnorm(x, None, r, layers[0]["input_layernorm"], eps)
+        if not masked and self._fused_moe():
+            k = cfg.num_experts_per_tok
+            for layer, w in enumerate(layers):
+                a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
+                weights, ids, z = route_add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps,
+                                                    w["block_sparse_moe.router.layer"], k, z)
+                y = self.ep.backend.routes(z, w["input_linear"], w["output_linear"], ids)
+                nxt = layers[layer + 1]["input_layernorm"] if layer + 1 < len(layers) else self.w["norm"]
+                finish_add_rmsnorm(y, ids, weights, x, r, nxt, eps, z)
+        else:
+            y = None
+            for layer, w in enumerate(layers):
+                if layer:
+                    add_rmsnorm(x, y, r, w["input_layernorm"], eps, out=z)
+                a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
+                if masked:
+                    a = a * valid_rows[:, None]
+                add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps, out=z)
+                scales, ids = route(z, w["block_sparse_moe.router.layer"], cfg.num_experts_per_tok)
+                y = self.ep(z, ids, scales, valid_rows, w["physical"], w["input_linear"], w["output_linear"],
+                            w["logical"], decode=True, tokens=communication_tokens)
+            z = add_rmsnorm(x, y, r, self.w["norm"], eps, out=z)
         if last is not None:
             index = last.long() if isinstance(last, torch.Tensor) else torch.tensor([last], device=x.device)
-            x, y = x[index].contiguous(), y[index].contiguous()
-            out_rows = (x.shape[0], 1)
+            z = z[index]
+            out_rows = (z.shape[0], 1)
         else:
             out_rows = (b, s)
-        z = add_rmsnorm(x, y, r, self.w["norm"], eps)
         return (F.linear(z, self.w["head"]) / cfg.logits_scaling).view(*out_rows, -1)

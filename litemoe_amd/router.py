@@ -51,3 +51,23 @@ def route(z, gate_weight, topk, renormalize=True, logits_out=None):
               int(bool(renormalize)), _lib.ptr(logits_out), weights.data_ptr(), ids.data_ptr(),
               _lib.stream(z.device))
     return weights, ids
+
+
+def add_rmsnorm_route(x, a, alpha, norm_weight, eps, gate_weight, topk, z=None, renormalize=True,
+                      logits_out=None):
+    """``x <- bf16(x + alpha * a)``, ``z = rmsnorm(x)``, then :func:`route` on z,
+    in one kernel (litemoe/model.py:108-113). Returns (weights, ids, z)."""
+    _lib.require_cuda(x, norm_weight, gate_weight, what="router inputs")
+    if x.dtype != torch.bfloat16 or not x.is_contiguous() or gate_weight.shape[1] != x.shape[-1]:
+        raise ValueError('Router needs a contiguous BF16 [M, H] residual and [E, H] weight')
+    if a is not None and (a.shape != x.shape or a.dtype != x.dtype or not a.is_contiguous()):
+        raise ValueError('Residual input must match x and be contiguous')
+    m, hidden = x.numel() // x.shape[-1], x.shape[-1]
+    experts = gate_weight.shape[0]
+    z = torch.empty_like(x) if z is None else z
+    weights, ids = _outputs(m, topk, x.device)
+    _lib.call("lm_add_rmsnorm_router", x.data_ptr(), _lib.ptr(a), float(alpha), norm_weight.data_ptr(),
+              float(eps), z.data_ptr(), gate_weight.data_ptr(), m, hidden, experts, topk,
+              int(bool(renormalize)), _lib.ptr(logits_out), weights.data_ptr(), ids.data_ptr(),
+              _lib.stream(x.device))
+    return weights, ids, z

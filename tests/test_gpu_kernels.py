@@ -245,13 +245,11 @@ def test_expert_stages_match_oracle(m, h, i, e, k):
     x, w1, w2, weights, ids = _moe_inputs(m, h, i, e, k, 100 + m)
     offsets, order, _ = experts.moe_align(ids.to(DEV), e)
     act = experts.gate_up(x.to(DEV), w1.to(DEV), offsets, order, k).cpu()
-    order_c = order.cpu().long()
-    rows = x[order_c // k]
+    flat = ids.flatten().long()
     exp_act = torch.empty_like(act)
-    for p in range(order_c.numel()):
-        ex = int(ids.flatten()[order_c[p]])
-        gate, up = torch.nn.functional.linear(rows[p:p + 1], w1[ex]).chunk(2, -1)
-        exp_act[p] = (torch.nn.functional.silu(gate) * up)[0]
+    for r in range(flat.numel()):
+        gate, up = torch.nn.functional.linear(x[r // k][None], w1[flat[r]]).chunk(2, -1)
+        exp_act[r] = (torch.nn.functional.silu(gate) * up)[0]
     assert rel_l2(act, exp_act) < 5e-3
     y = experts.down(act.to(DEV), w2.to(DEV), offsets, order).cpu()
     ey = ops.expert_routes(x, ids, w1, w2)
@@ -402,3 +400,55 @@ def test_prefill_attention_matches_oracle_and_isolates_sequences(lengths):
     assert torch.equal(changed[:start], got[:start]) and torch.equal(changed[end:], got[end:])
     assert torch.equal(changed[start:1], got[start:1])
     assert not torch.equal(changed[1:end], got[1:end])
+
+
+# ----------------------------------------------------------- fused decode ops --
+
+@pytest.mark.parametrize("m", [1, 16, 64, 256, 257])
+@torch.inference_mode()
+def test_moe_routes_scan_path_equals_block_path(m):
+    """The decode path (each expert collects its own routes, m <= 256) and the
+    aligned-block path give bit-identical route outputs."""
+    x, w1, w2, weights, ids = _moe_inputs(m, 1536, 512, 40, 8, 300 + m)
+    args = [t.to(DEV) for t in (x, w1, w2)]
+    scan = experts.moe_routes(*args, ids.to(DEV))
+    blocks = experts.moe_routes(*args, ids.to(DEV), block_rows=16)
+    assert torch.equal(scan, blocks)
+    if m <= 16:
+        assert rel_l2(scan.cpu(), ops.expert_routes(x, ids, w1, w2)) < 1e-2
+
+
+@torch.inference_mode()
+def test_finish_add_rmsnorm_equals_unfused():
+    m, h, k, e = 64, 1536, 8, 40
+    g = torch.Generator().manual_seed(12)
+    y = torch.randn(m * k, h, generator=g).to(torch.bfloat16).to(DEV)
+    ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(m)]).int().to(DEV)
+    scales = torch.softmax(torch.randn(m, k, generator=g), -1).to(DEV)
+    x = torch.randn(m, h, generator=g).to(torch.bfloat16).to(DEV)
+    w = (1 + 0.2 * torch.randn(h, generator=g)).to(torch.bfloat16).to(DEV)
+    x1, x2 = x.clone(), x.clone()
+    z1 = experts.finish_add_rmsnorm(y, ids, scales, x1, 0.22, w, 1e-6)
+    out = torch.empty(m, h, device=DEV, dtype=torch.bfloat16)
+    moe_finish.finish(y, ids, torch.arange(m * k, device=DEV), scales, out, 0, e)
+    z2 = norm.add_rmsnorm(x2, out, 0.22, w, 1e-6)
+    assert torch.equal(x1, x2) and torch.equal(z1, z2)
+
+
+@pytest.mark.parametrize("with_residual", [False, True])
+@torch.inference_mode()
+def test_add_rmsnorm_route_equals_unfused(with_residual):
+    m, h, e, k = 64, 1536, 40, 8
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(m, h, generator=g).to(torch.bfloat16).to(DEV)
+    a = torch.randn(m, h, generator=g).to(torch.bfloat16).to(DEV) if with_residual else None
+    w = (1 + 0.2 * torch.randn(h, generator=g)).to(torch.bfloat16).to(DEV)
+    wr = (0.02 * torch.randn(e, h, generator=g)).to(torch.bfloat16).to(DEV)
+    x1, x2 = x.clone(), x.clone()
+    logits1 = torch.empty(m, e, device=DEV, dtype=torch.bfloat16)
+    w1_, i1, z1 = router.add_rmsnorm_route(x1, a, 0.22, w, 1e-6, wr, k, logits_out=logits1)
+    z2 = norm.add_rmsnorm(x2, a, 0.22, w, 1e-6)
+    logits2 = torch.empty(m, e, device=DEV, dtype=torch.bfloat16)
+    w2_, i2 = router.route(z2, wr, k, logits_out=logits2)
+    assert torch.equal(x1, x2) and torch.equal(z1, z2) and torch.equal(logits1, logits2)
+    assert torch.equal(i1, i2) and torch.equal(w1_, w2_)
