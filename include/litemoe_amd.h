@@ -87,7 +87,8 @@ int lm_kv_write(const void *k, int64_t ks0, int64_t ks1, int64_t ks3,
  * Replaces vLLM `_custom_ops.rotary_embedding(positions, q, k, D, cos_sin,
  * is_neox=True)` at litemoe/model.py:58,63-64 followed by `cache.write`
  * (model.py:59,70 -> kv_write.py:23-29). q, k, v rows have a row stride and a
- * head stride; channels are contiguous. head_dim must be 64. With k_cache and
+ * head stride (multiples of 8 elements, 16-byte aligned rows); channels are
+ * contiguous. head_dim must be 64. With k_cache and
  * v_cache both NULL nothing is stored (v and active may then be NULL): the
  * call is vLLM's in-place rotary_embedding alone. */
 int lm_rope_kv_write(void *q, int64_t qs0, int64_t qs1, void *k, int64_t ks0,
@@ -151,7 +152,9 @@ int lm_prefill_attention(const void *q, int64_t qs0, int64_t qs1,
  * (litemoe/model.py:110, ops.py:7-12) and vLLM `fused_topk(z, scores, k,
  * renormalize=True)` (model.py:111-113); on the CPU path `topk` + softmax
  * (model.py:115-116). x: [tokens, hidden] bf16, Wr: [experts, hidden] bf16,
- * hidden % 8 == 0, experts <= 256, topk <= min(experts, 16). */
+ * hidden % 8 == 0, hidden <= 4096, experts <= 256, topk <= min(experts, 16).
+ * Ties among the selected are ordered by id; the weights' denominator is
+ * summed in selection order. */
 int lm_router(const void *x, const void *gate_weight, int64_t tokens,
               int64_t hidden, int64_t experts, int64_t topk, int renormalize,
               void *logits_out, float *topk_weights, int32_t *topk_ids,

@@ -39,26 +39,42 @@ finish_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ ids,
     for (int i = 0; i < kMaxK; ++i) r += key[i] < key[j];
     order[j] = r;
   }
+  // All loads first (scales and the owned rows), then the ordered sum; the
+  // order is the same for every thread of the token, so the branches are
+  // uniform.
+  float contrib[kMaxK][kCols];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j) {
+    const int64_t r = t * topk + j;
+    const int64_t e = j < topk ? (int64_t)ids[r] - rank * count : -1;
+    const bool use = j < topk && e >= 0 && e < count;
+    const float s = use ? round_bf16(scales[r]) : 0.f;
+    if (use) {
+      const bf16 *yr = y + (inverse ? (int64_t)inverse[r] : r) * hidden + c0;
+      if constexpr (kCols == 8) {
+        float v[8];
+        unpack8(*reinterpret_cast<const u32x4 *>(yr), v);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) contrib[j][c] = round_bf16(v[c] * s);
+      } else {
+        contrib[j][0] = round_bf16(bf16_to_f32(yr[0]) * s);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < kCols; ++c) contrib[j][c] = 0.f;
+    }
+  }
   float total[kCols];
 #pragma unroll
   for (int c = 0; c < kCols; ++c) total[c] = 0.f;
-  for (int q = 0; q < topk; ++q) {
-    int sel = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxK; ++j) sel += (order[j] == q) ? j : 0;
-    const int64_t r = t * topk + sel;
-    const int64_t e = (int64_t)ids[r] - rank * count;
-    if (e < 0 || e >= count) continue;
-    const int64_t row = inverse ? (int64_t)inverse[r] : r;
-    const float s = round_bf16(scales[r]);
-    const bf16 *yr = y + row * hidden + c0;
-    if constexpr (kCols == 8) {
-      float v[8];
-      unpack8(*reinterpret_cast<const u32x4 *>(yr), v);
+  for (int q = 0; q < kMaxK; ++q) {
 #pragma unroll
-      for (int c = 0; c < 8; ++c) total[c] += round_bf16(v[c] * s);
-    } else {
-      total[0] += round_bf16(bf16_to_f32(yr[0]) * s);
+    for (int j = 0; j < kMaxK; ++j) {
+      if (order[j] == q) {
+#pragma unroll
+        for (int c = 0; c < kCols; ++c) total[c] += contrib[j][c];
+      }
     }
   }
   bf16 *o = out + t * hidden + c0;
@@ -108,17 +124,31 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
   for (int v = 0; v < kMaxVec; ++v) {
     const int i = threadIdx.x + v * 256;
     if (i >= nvec) continue;
+    float contrib[kMaxK][8];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      if (j < topk) {
+        const int64_t r = t * topk + j;
+        const float s = round_bf16(scales[r]);
+        float f[8];
+        unpack8(reinterpret_cast<const u32x4 *>(y + r * hidden)[i], f);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) contrib[j][c] = round_bf16(f[c] * s);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) contrib[j][c] = 0.f;
+      }
+    }
     float total[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int q = 0; q < topk; ++q) {
-      int sel = 0;
 #pragma unroll
-      for (int j = 0; j < kMaxK; ++j) sel += (order[j] == q) ? j : 0;
-      const int64_t r = t * topk + sel;
-      const float s = round_bf16(scales[r]);
-      float f[8];
-      unpack8(reinterpret_cast<const u32x4 *>(y + r * hidden)[i], f);
+    for (int q = 0; q < kMaxK; ++q) {
 #pragma unroll
-      for (int c = 0; c < 8; ++c) total[c] += round_bf16(f[c] * s);
+      for (int j = 0; j < kMaxK; ++j) {
+        if (order[j] == q) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) total[c] += contrib[j][c];
+        }
+      }
     }
     float xv[8];
     unpack8(reinterpret_cast<const u32x4 *>(x + t * hidden)[i], xv);

@@ -123,8 +123,10 @@ __device__ __forceinline__ void rotate(float x1, float x2, float c, float s, flo
   o2 = round_bf16(round_bf16(x2 * c) + round_bf16(x1 * s));
 }
 
-// One workgroup per row; head_dim 64 -> 32 pairs per head. Work items:
-// q pairs [0, Hq*32), k pairs [Hq*32, (Hq+Hkv)*32), v channels after that.
+// One workgroup per row; head_dim 64. Work items are 16-byte channel units:
+// a rotation item is the unit pair (channels 8u..8u+7, 32+8u..32+8u+7),
+// u < 4, of one q or k head; a v item is one unit of a v head. Every load of
+// an item is issued before any arithmetic.
 __global__ void __launch_bounds__(256)
 rope_kv_kernel(bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__restrict__ k, int64_t ks0,
                int64_t ks1, const bf16 *__restrict__ v, int64_t vs0, int64_t vs1,
@@ -140,30 +142,47 @@ rope_kv_kernel(bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__restrict_
                      slot < cache_batch;
   const bool in_table = p >= 0 && p < table_len;
   const bf16 *cs = cos_sin + (in_table ? p : 0) * D;
-  const int nq = q_heads * P, nk = kv_heads * P, nv = kv_heads * D;
+  const int nq = q_heads * 4, nk = kv_heads * 4, nv = kv_heads * 8;
   for (int item = threadIdx.x; item < nq + nk + nv; item += 256) {
     if (item < nq + nk) {
       const bool is_q = item < nq;
       const int j = is_q ? item : item - nq;
-      const int h = j / P, i = j % P;
+      const int h = j / 4, u = j % 4;
       bf16 *base = is_q ? q + row * qs0 + h * qs1 : k + row * ks0 + h * ks1;
-      const float x1 = bf16_to_f32(base[i]), x2 = bf16_to_f32(base[i + P]);
-      float o1 = x1, o2 = x2;
-      if (in_table) rotate(x1, x2, bf16_to_f32(cs[i]), bf16_to_f32(cs[P + i]), o1, o2);
-      const bf16 b1 = (bf16)f32_to_bf16(o1), b2 = (bf16)f32_to_bf16(o2);
+      const u32x4 w1 = *reinterpret_cast<const u32x4 *>(base + 8 * u);
+      const u32x4 w2 = *reinterpret_cast<const u32x4 *>(base + P + 8 * u);
+      const u32x4 wc = *reinterpret_cast<const u32x4 *>(cs + 8 * u);
+      const u32x4 ws = *reinterpret_cast<const u32x4 *>(cs + P + 8 * u);
+      float x1[8], x2[8], c[8], sn[8];
+      unpack8(w1, x1);
+      unpack8(w2, x2);
+      unpack8(wc, c);
+      unpack8(ws, sn);
+      u32x4 o1 = w1, o2 = w2;
+      if (in_table) {
+        float r1[8], r2[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rotate(x1[i], x2[i], c[i], sn[i], r1[i], r2[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o1[i] = pack_bf16(r1[2 * i], r1[2 * i + 1]);
+          o2[i] = pack_bf16(r2[2 * i], r2[2 * i + 1]);
+        }
+      }
       if (is_q || write_k) {
-        base[i] = b1;
-        base[i + P] = b2;
+        *reinterpret_cast<u32x4 *>(base + 8 * u) = o1;
+        *reinterpret_cast<u32x4 *>(base + P + 8 * u) = o2;
       }
       if (!is_q && store) {
         bf16 *dst = kc + ((slot * kv_heads + h) * capacity + p) * D;
-        dst[i] = b1;
-        dst[i + P] = b2;
+        *reinterpret_cast<u32x4 *>(dst + 8 * u) = o1;
+        *reinterpret_cast<u32x4 *>(dst + P + 8 * u) = o2;
       }
     } else if (store) {
       const int j = item - nq - nk;
-      const int h = j / D, c = j % D;
-      vc[((slot * kv_heads + h) * capacity + p) * D + c] = v[row * vs0 + h * vs1 + c];
+      const int h = j / 8, u = j % 8;
+      *reinterpret_cast<u32x4 *>(vc + ((slot * kv_heads + h) * capacity + p) * D + 8 * u) =
+          *reinterpret_cast<const u32x4 *>(v + row * vs0 + h * vs1 + 8 * u);
     }
   }
 }

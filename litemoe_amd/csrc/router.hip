@@ -12,12 +12,15 @@ namespace lm {
 namespace {
 
 constexpr int kRouterThreads = 256;
-constexpr int kMaxExperts = 256;
+constexpr int kRouterWaves = kRouterThreads / kWave;
+constexpr int kMaxExperts = 256;  // one selecting thread per expert
 constexpr int kMaxTopk = 16;
+constexpr int kMaxNormVec = 2;    // hidden <= kMaxNormVec * 8 * kRouterThreads
+constexpr int kExpertBatch = 5;   // experts whose weight loads one wave keeps in flight
 
 // Monotone map float -> uint32 (NaN canonicalised above +inf, as torch.topk
-// orders NaN first), combined with the inverted expert id so that a 64-bit
-// max picks the largest value and, among equals, the lowest id.
+// orders NaN first), combined with the inverted expert id so that a larger
+// 64-bit key means a larger value or, for equal values, a lower id.
 __device__ __forceinline__ uint64_t select_key(float v, int e) {
   uint32_t u = __float_as_uint(v);
   if ((u & 0x7fffffffu) > 0x7f800000u) u = 0x7fc00000u;
@@ -25,108 +28,113 @@ __device__ __forceinline__ uint64_t select_key(float v, int e) {
   return ((uint64_t)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+// logit[e] = bf16(z . W_r[e]) for all experts; z (nvec 16-byte words) is in
+// LDS. Wave w takes experts w, w+4, ... in batches of kExpertBatch whose
+// weight loads are issued together.
+__device__ void router_gemv(const u32x4 *zs, const bf16 *__restrict__ wr, int nvec, int experts,
+                            float *logit, bf16 *__restrict__ logits_row) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int per_wave = (experts - wave + kRouterWaves - 1) / kRouterWaves;
+  for (int j0 = 0; j0 < per_wave; j0 += kExpertBatch) {
+    float acc[kExpertBatch];
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const uint32_t hi = shfl_xor((uint32_t)(v >> 32), m);
-    const uint32_t lo = shfl_xor((uint32_t)v, m);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-// Executed by one full wave. logit[e] (e < experts) holds bf16-rounded
-// logits as floats. Writes topk weights and ids of one token.
-__device__ void select_topk(const float *logit, int experts, int topk, int renormalize,
-                            float *__restrict__ tw, int32_t *__restrict__ tid) {
-  const int lane = threadIdx.x % kWave;
-  uint64_t cand[kMaxExperts / kWave];
+    for (int b = 0; b < kExpertBatch; ++b) acc[b] = 0.f;
+    for (int i = lane; i < nvec; i += kWave) {
+      float zf[8];
+      unpack8(zs[i], zf);
+      u32x4 w[kExpertBatch];
 #pragma unroll
-  for (int c = 0; c < kMaxExperts / kWave; ++c) {
-    const int e = lane + c * kWave;
-    cand[c] = e < experts ? select_key(logit[e], e) : 0ull;
-  }
-  // Lane j keeps the j-th selection; every lane sees the running maximum.
-  float mine = 0.f, m = 0.f;
-  int mine_id = 0;
-  for (int j = 0; j < topk; ++j) {
-    uint64_t best = 0ull;
+      for (int b = 0; b < kExpertBatch; ++b) {
+        const int e = wave + (j0 + b) * kRouterWaves;
+        const int ee = e < experts ? e : wave;
+        w[b] = reinterpret_cast<const u32x4 *>(wr + (int64_t)ee * nvec * 8)[i];
+      }
 #pragma unroll
-    for (int c = 0; c < kMaxExperts / kWave; ++c) best = cand[c] > best ? cand[c] : best;
-    best = wave_max_u64(best);
-    const int e = (int)(0xffffffffu - (uint32_t)best);
-    const float v = logit[e];
-    if (j == 0) m = v;
-    if (lane == j) {
-      mine = v;
-      mine_id = e;
+      for (int b = 0; b < kExpertBatch; ++b) {
+        float wf[8];
+        unpack8(w[b], wf);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[b] = fmaf(zf[c], wf[c], acc[b]);
+      }
     }
 #pragma unroll
-    for (int c = 0; c < kMaxExperts / kWave; ++c)
-      if (cand[c] == best) cand[c] = 0ull;
-  }
-  const float ex = lane < topk ? expf(mine - m) : 0.f;
-  float denom;
-  if (renormalize) {
-    denom = wave_sum(ex);
-  } else {
-    float part = 0.f;
-    for (int e = lane; e < experts; e += kWave) part += expf(logit[e] - m);
-    denom = wave_sum(part);
-  }
-  if (lane < topk) {
-    tw[lane] = ex / denom;
-    tid[lane] = mine_id;
+    for (int b = 0; b < kExpertBatch; ++b) {
+      const int e = wave + (j0 + b) * kRouterWaves;
+      const float sum = wave_sum(acc[b]);
+      if (lane == 0 && e < experts) {
+        const uint32_t h = f32_to_bf16(sum);
+        logit[e] = bf16_to_f32(h);
+        if (logits_row) logits_row[e] = (bf16)h;
+      }
+    }
   }
 }
 
-// One workgroup per token; wave w computes logits of experts w, w+4, ...
+// Top-k by rank: thread t (one per expert) counts the experts with a larger
+// key; ranks are distinct, so rank < topk places expert t at that position.
+// Weights: softmax over the selection (renormalize) or over all logits,
+// with the denominator summed in a fixed order. Synchronises.
+__device__ void select_topk(const float *logit, int experts, int topk, int renormalize,
+                            float *sel_val, int *sel_id, float *__restrict__ tw,
+                            int32_t *__restrict__ tid) {
+  const int t = threadIdx.x;
+  if (t < experts) {
+    const uint64_t mine = select_key(logit[t], t);
+    int rank = 0;
+    for (int e = 0; e < experts; ++e) rank += select_key(logit[e], e) > mine;
+    if (rank < topk) {
+      sel_val[rank] = logit[t];
+      sel_id[rank] = t;
+    }
+  }
+  __syncthreads();
+  if (t < topk) {
+    const float m = sel_val[0];
+    float denom = 0.f;
+    if (renormalize) {
+      for (int j = 0; j < topk; ++j) denom += expf(sel_val[j] - m);
+    } else {
+      for (int e = 0; e < experts; ++e) denom += expf(logit[e] - m);
+    }
+    tw[t] = expf(sel_val[t] - m) / denom;
+    tid[t] = sel_id[t];
+  }
+}
+
+// One workgroup per token: stage the row in LDS, GEMV, select.
 __global__ void __launch_bounds__(kRouterThreads)
 router_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ wr, int hidden, int experts,
               int topk, int renormalize, bf16 *__restrict__ logits_out, float *__restrict__ tw,
               int32_t *__restrict__ tid) {
+  __shared__ u32x4 zs[kMaxNormVec * kRouterThreads];
   __shared__ float logit[kMaxExperts];
+  __shared__ float sel_val[kMaxTopk];
+  __shared__ int sel_id[kMaxTopk];
   const int64_t row = blockIdx.x;
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int nvec = hidden / 8;
-  const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + row * hidden);
-  for (int e = wave; e < experts; e += kRouterThreads / kWave) {
-    const u32x4 *w = reinterpret_cast<const u32x4 *>(wr + (int64_t)e * hidden);
-    float acc = 0.f;
-    for (int i = lane; i < nvec; i += kWave) {
-      float a[8], b[8];
-      unpack8(xr[i], a);
-      unpack8(w[i], b);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc = fmaf(a[j], b[j], acc);
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) {
-      const uint32_t h = f32_to_bf16(acc);
-      logit[e] = bf16_to_f32(h);
-      if (logits_out) logits_out[row * experts + e] = (bf16)h;
-    }
-  }
+  for (int i = threadIdx.x; i < nvec; i += kRouterThreads)
+    zs[i] = reinterpret_cast<const u32x4 *>(x + row * hidden)[i];
   __syncthreads();
-  if (wave == 0) select_topk(logit, experts, topk, renormalize, tw + row * topk, tid + row * topk);
+  router_gemv(zs, wr, nvec, experts, logit, logits_out ? logits_out + row * experts : nullptr);
+  __syncthreads();
+  select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
 }
 
-__global__ void __launch_bounds__(kWave)
+__global__ void __launch_bounds__(kRouterThreads)
 topk_from_logits_kernel(const bf16 *__restrict__ logits, int experts, int topk, int renormalize,
                         float *__restrict__ tw, int32_t *__restrict__ tid) {
   __shared__ float logit[kMaxExperts];
+  __shared__ float sel_val[kMaxTopk];
+  __shared__ int sel_id[kMaxTopk];
   const int64_t row = blockIdx.x;
-  for (int e = threadIdx.x; e < experts; e += kWave) logit[e] = bf16_to_f32(logits[row * experts + e]);
+  for (int e = threadIdx.x; e < experts; e += kRouterThreads)
+    logit[e] = bf16_to_f32(logits[row * experts + e]);
   __syncthreads();
-  select_topk(logit, experts, topk, renormalize, tw + row * topk, tid + row * topk);
+  select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
 }
 
 // Residual add + RMSNorm + router GEMV + top-k, one workgroup per token.
-// The normalised row stays in LDS for the GEMV; wave w computes the logits of
-// experts w, w+4, ... two at a time.
-constexpr int kMaxNormVec = 2;  // hidden <= kMaxNormVec * 8 * kRouterThreads
-
+// The normalised row stays in LDS for the GEMV.
 __global__ void __launch_bounds__(kRouterThreads)
 add_norm_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha,
                        const bf16 *__restrict__ nw, float eps, bf16 *__restrict__ z,
@@ -135,7 +143,9 @@ add_norm_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float a
                        int32_t *__restrict__ tid) {
   __shared__ u32x4 zs[kMaxNormVec * kRouterThreads];
   __shared__ float logit[kMaxExperts];
-  __shared__ float red[kRouterThreads / kWave];
+  __shared__ float red[kRouterWaves];
+  __shared__ float sel_val[kMaxTopk];
+  __shared__ int sel_id[kMaxTopk];
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int nvec = hidden / 8;
@@ -165,7 +175,7 @@ add_norm_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float a
   __syncthreads();
   float total = 0.f;
 #pragma unroll
-  for (int w = 0; w < kRouterThreads / kWave; ++w) total += red[w];
+  for (int w = 0; w < kRouterWaves; ++w) total += red[w];
   const float scale = 1.0f / sqrtf(total / (float)hidden + eps);
 #pragma unroll
   for (int v = 0; v < kMaxNormVec; ++v) {
@@ -182,37 +192,9 @@ add_norm_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float a
     reinterpret_cast<u32x4 *>(z + row * hidden)[i] = o;
   }
   __syncthreads();
-  for (int e0 = wave; e0 < experts; e0 += 2 * (kRouterThreads / kWave)) {
-    const int e1 = e0 + kRouterThreads / kWave;
-    const bool two = e1 < experts;
-    const u32x4 *w0 = reinterpret_cast<const u32x4 *>(wr + (int64_t)e0 * hidden);
-    const u32x4 *w1 = reinterpret_cast<const u32x4 *>(wr + (int64_t)(two ? e1 : e0) * hidden);
-    float acc0 = 0.f, acc1 = 0.f;
-    for (int i = lane; i < nvec; i += kWave) {
-      float zf[8], b0[8], b1[8];
-      unpack8(zs[i], zf);
-      unpack8(w0[i], b0);
-      unpack8(w1[i], b1);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        acc0 = fmaf(zf[c], b0[c], acc0);
-        acc1 = fmaf(zf[c], b1[c], acc1);
-      }
-    }
-    acc0 = wave_sum(acc0);
-    acc1 = wave_sum(acc1);
-    if (lane == 0) {
-      const uint32_t h0 = f32_to_bf16(acc0), h1 = f32_to_bf16(acc1);
-      logit[e0] = bf16_to_f32(h0);
-      if (logits_out) logits_out[row * experts + e0] = (bf16)h0;
-      if (two) {
-        logit[e1] = bf16_to_f32(h1);
-        if (logits_out) logits_out[row * experts + e1] = (bf16)h1;
-      }
-    }
-  }
+  router_gemv(zs, wr, nvec, experts, logit, logits_out ? logits_out + row * experts : nullptr);
   __syncthreads();
-  if (wave == 0) select_topk(logit, experts, topk, renormalize, tw + row * topk, tid + row * topk);
+  select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
 }
 
 constexpr int kAlignThreads = 1024;
@@ -319,7 +301,8 @@ extern "C" int lm_router(const void *x, const void *gate_weight, int64_t tokens,
                          int64_t experts, int64_t topk, int renormalize, void *logits_out,
                          float *topk_weights, int32_t *topk_ids, void *stream) {
   LM_REQUIRE(tokens >= 0 && hidden > 0 && experts > 0 && topk > 0);
-  if (hidden % 8 || experts > kMaxExperts || topk > kMaxTopk || topk > experts)
+  if (hidden % 8 || hidden > kMaxNormVec * 8 * kRouterThreads || experts > kMaxExperts ||
+      topk > kMaxTopk || topk > experts)
     return LM_EUNSUPPORTED;
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(x && gate_weight && topk_weights && topk_ids);
@@ -356,7 +339,7 @@ extern "C" int lm_topk_softmax(const void *logits, int64_t tokens, int64_t exper
   if (experts > kMaxExperts || topk > kMaxTopk || topk > experts) return LM_EUNSUPPORTED;
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(logits && topk_weights && topk_ids);
-  topk_from_logits_kernel<<<dim3((unsigned)tokens), kWave, 0, (hipStream_t)stream>>>(
+  topk_from_logits_kernel<<<dim3((unsigned)tokens), kRouterThreads, 0, (hipStream_t)stream>>>(
       (const bf16 *)logits, (int)experts, (int)topk, renormalize, topk_weights, topk_ids);
   LM_CHECK_LAUNCH();
   return LM_OK;

@@ -19,6 +19,9 @@ def _check(q, k, cos_sin, positions):
         raise ValueError('RoPE needs contiguous channels and a contiguous cos/sin table')
     if q.shape[-1] != 64 or k.shape[-1] != 64 or cos_sin.shape[-1] != 64:
         raise ValueError('RoPE kernel supports head_dim 64')
+    for t in (q, k):
+        if t.stride(0) % 8 or t.stride(1) % 8 or t.data_ptr() % 16:
+            raise ValueError('RoPE needs 16-byte aligned rows and heads (strides multiple of 8)')
 
 
 def rotary_embedding(positions, query, key, head_size, cos_sin_cache, is_neox=True):
@@ -46,6 +49,8 @@ def rope_kv_write(q, k, v, positions, active, cos_sin, cache, layer, slots=None,
     kc, vc = cache.k[layer], cache.v[layer]
     if v.stride(-1) != 1 or v.dtype != torch.bfloat16 or kc.dtype != torch.bfloat16:
         raise ValueError('Fused RoPE/KV write needs BF16 v and cache with contiguous channels')
+    if v.stride(0) % 8 or v.stride(1) % 8 or v.data_ptr() % 16:
+        raise ValueError('RoPE needs 16-byte aligned v rows and heads (strides multiple of 8)')
     rows = q.shape[0]
     positions = positions.to(torch.int64).contiguous()
     active = active.to(torch.bool).contiguous()
