@@ -89,9 +89,14 @@ finish_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ ids,
 }
 
 // Finish fused with the residual add and the next RMSNorm; one workgroup per
-// token, 8 columns per thread, hidden <= kMaxVec * 8 * 256.
+// token, 8 columns per thread, hidden <= kMaxVec * 8 * 256. Every load (ids,
+// scales, the token's route rows, the residual row, the norm weight) is
+// issued at entry with clamped indices, so the kernel waits on memory once;
+// the arithmetic and the reduction order are those of finish_kernel followed
+// by rmsnorm_kernel.
 constexpr int kMaxVec = 2;
 
+template <int NN>
 __global__ void __launch_bounds__(256)
 finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ ids,
                        const float *__restrict__ scales, const int64_t *__restrict__ logical,
@@ -99,16 +104,31 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
                        float eps, bf16 *__restrict__ z, int hidden, int topk) {
   __shared__ float red[4];
   const int64_t t = blockIdx.x;
-  int64_t key[kMaxK];
+  const int nvec = hidden / 8;
+  int idv[kMaxK];
+  float sc[kMaxK];
 #pragma unroll
   for (int j = 0; j < kMaxK; ++j) {
-    if (j < topk) {
-      const int64_t e = ids[t * topk + j];
-      key[j] = (logical ? logical[e] : e) * topk + j;
-    } else {
-      key[j] = INT64_MAX;
-    }
+    const int64_t r = t * topk + (j < topk ? j : topk - 1);
+    idv[j] = ids[r];
+    sc[j] = scales[r];
   }
+  u32x4 yv[NN][kMaxK], xv[NN], wv[NN];
+#pragma unroll
+  for (int v = 0; v < NN; ++v) {
+    const int i = min((int)threadIdx.x + v * 256, nvec - 1);
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      const int64_t r = t * topk + (j < topk ? j : topk - 1);
+      yv[v][j] = reinterpret_cast<const u32x4 *>(y + r * hidden)[i];
+    }
+    xv[v] = reinterpret_cast<const u32x4 *>(x + t * hidden)[i];
+    wv[v] = reinterpret_cast<const u32x4 *>(w)[i];
+  }
+  int64_t key[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j)
+    key[j] = j < topk ? (logical ? logical[idv[j]] : (int64_t)idv[j]) * topk + j : INT64_MAX;
   int order[kMaxK];
 #pragma unroll
   for (int j = 0; j < kMaxK; ++j) {
@@ -117,27 +137,20 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
     for (int i = 0; i < kMaxK; ++i) r += key[i] < key[j];
     order[j] = r;
   }
-  const int nvec = hidden / 8;
-  float xn[kMaxVec][8];
+  float xn[NN][8];
   float ss = 0.f;
 #pragma unroll
-  for (int v = 0; v < kMaxVec; ++v) {
+  for (int v = 0; v < NN; ++v) {
     const int i = threadIdx.x + v * 256;
     if (i >= nvec) continue;
     float contrib[kMaxK][8];
 #pragma unroll
     for (int j = 0; j < kMaxK; ++j) {
-      if (j < topk) {
-        const int64_t r = t * topk + j;
-        const float s = round_bf16(scales[r]);
-        float f[8];
-        unpack8(reinterpret_cast<const u32x4 *>(y + r * hidden)[i], f);
+      const float s = round_bf16(sc[j]);
+      float f[8];
+      unpack8(yv[v][j], f);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) contrib[j][c] = round_bf16(f[c] * s);
-      } else {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) contrib[j][c] = 0.f;
-      }
+      for (int c = 0; c < 8; ++c) contrib[j][c] = j < topk ? round_bf16(f[c] * s) : 0.f;
     }
     float total[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -150,12 +163,12 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
         }
       }
     }
-    float xv[8];
-    unpack8(reinterpret_cast<const u32x4 *>(x + t * hidden)[i], xv);
+    float xf[8];
+    unpack8(xv[v], xf);
     u32x4 o;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      xn[v][c] = round_bf16(xv[c] + alpha * round_bf16(total[c]));
+      xn[v][c] = round_bf16(xf[c] + alpha * round_bf16(total[c]));
       ss += xn[v][c] * xn[v][c];
     }
 #pragma unroll
@@ -167,11 +180,11 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
   __syncthreads();
   const float scale = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)hidden + eps);
 #pragma unroll
-  for (int v = 0; v < kMaxVec; ++v) {
+  for (int v = 0; v < NN; ++v) {
     const int i = threadIdx.x + v * 256;
     if (i >= nvec) continue;
     float g[8];
-    unpack8(reinterpret_cast<const u32x4 *>(w)[i], g);
+    unpack8(wv[v], g);
     u32x4 o;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -242,9 +255,14 @@ extern "C" int lm_moe_finish_add_rmsnorm(const void *y, const int32_t *ids, cons
   if (hidden % 8 || hidden > kMaxVec * 8 * 256) return LM_EUNSUPPORTED;
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(y && ids && scales && x && norm_weight && z);
-  finish_add_norm_kernel<<<dim3((unsigned)tokens), 256, 0, (hipStream_t)stream>>>(
-      (const bf16 *)y, ids, scales, logical, (bf16 *)x, alpha, (const bf16 *)norm_weight, eps,
-      (bf16 *)z, (int)hidden, (int)topk);
+  if (hidden <= 8 * 256)
+    finish_add_norm_kernel<1><<<dim3((unsigned)tokens), 256, 0, (hipStream_t)stream>>>(
+        (const bf16 *)y, ids, scales, logical, (bf16 *)x, alpha, (const bf16 *)norm_weight, eps,
+        (bf16 *)z, (int)hidden, (int)topk);
+  else
+    finish_add_norm_kernel<2><<<dim3((unsigned)tokens), 256, 0, (hipStream_t)stream>>>(
+        (const bf16 *)y, ids, scales, logical, (bf16 *)x, alpha, (const bf16 *)norm_weight, eps,
+        (bf16 *)z, (int)hidden, (int)topk);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

@@ -197,6 +197,186 @@ add_norm_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float a
   select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
 }
 
+// Latency-bound variant for hidden = 512 * NV: 1024 threads, and every load
+// the row needs (the row, the residual, the norm weight and the first round
+// of gate rows) is issued at entry, so the kernel waits on memory once.
+// The norm runs on the first 256 threads with the reduction order of
+// rmsnorm_kernel, and the dot products keep router_gemv's order, so logits
+// and z are bitwise those of the unfused kernels.
+constexpr int kFastThreads = 1024;
+constexpr int kFastWaves = kFastThreads / kWave;
+
+template <int NV>
+struct FastRouter {
+  static constexpr int kBatch = 12 / NV > 4 ? 4 : (12 / NV < 1 ? 1 : 12 / NV);  // gate rows per wave per round
+  static constexpr int kRound = kBatch * kFastWaves;                        // experts per round
+  static constexpr int kNvec = NV * kWave;                                  // 16-byte words per row
+  static constexpr int kNorm = (kNvec + kRouterThreads - 1) / kRouterThreads;
+};
+
+template <int NV>
+__device__ __forceinline__ void load_gate_round(const bf16 *__restrict__ wr, int experts, int round,
+                                                u32x4 (&w)[FastRouter<NV>::kBatch][NV]) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int b = 0; b < FastRouter<NV>::kBatch; ++b) {
+    const int e = round * FastRouter<NV>::kRound + wave + b * kFastWaves;
+    const u32x4 *row = reinterpret_cast<const u32x4 *>(wr) +
+                       (int64_t)(e < experts ? e : 0) * FastRouter<NV>::kNvec;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) w[b][v] = row[lane + v * kWave];
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void gate_round(const u32x4 *zs, int experts, int round,
+                                           const u32x4 (&w)[FastRouter<NV>::kBatch][NV],
+                                           float *logit, bf16 *__restrict__ logits_row) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int b = 0; b < FastRouter<NV>::kBatch; ++b) {
+    const int e = round * FastRouter<NV>::kRound + wave + b * kFastWaves;
+    float acc = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      float zf[8], wf[8];
+      unpack8(zs[lane + v * kWave], zf);
+      unpack8(w[b][v], wf);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc = fmaf(zf[c], wf[c], acc);
+    }
+    const float sum = wave_sum(acc);
+    if (lane == 0 && e < experts) {
+      const uint32_t h = f32_to_bf16(sum);
+      logit[e] = bf16_to_f32(h);
+      if (logits_row) logits_row[e] = (bf16)h;
+    }
+  }
+}
+
+// kNorm: z = rmsnorm(x [+ alpha*a]) is routed (and x, z are written);
+// otherwise x itself is routed.
+template <int NV, bool kNorm, bool kAdd>
+__global__ void __launch_bounds__(kFastThreads)
+fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha,
+                   const bf16 *__restrict__ nw, float eps, bf16 *__restrict__ z,
+                   const bf16 *__restrict__ wr, int experts, int topk, int renormalize,
+                   bf16 *__restrict__ logits_out, float *__restrict__ tw,
+                   int32_t *__restrict__ tid) {
+  typedef FastRouter<NV> F;
+  constexpr int nvec = F::kNvec, NN = F::kNorm;
+  __shared__ u32x4 zs[nvec];
+  __shared__ float logit[kMaxExperts];
+  __shared__ float red[kRouterWaves];
+  __shared__ float sel_val[kMaxTopk];
+  __shared__ int sel_id[kMaxTopk];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  const bool norm_wave = t < kRouterThreads;
+  u32x4 *xr = reinterpret_cast<u32x4 *>(x + row * nvec * 8);
+  const u32x4 *ar = reinterpret_cast<const u32x4 *>(a + row * nvec * 8);
+  const u32x4 *gr = reinterpret_cast<const u32x4 *>(nw);
+  u32x4 xv[NN], av[NN], gv[NN];
+  if (norm_wave) {
+#pragma unroll
+    for (int v = 0; v < NN; ++v) {
+      const int i = min(t + v * kRouterThreads, nvec - 1);
+      xv[v] = xr[i];
+      if constexpr (kAdd) av[v] = ar[i];
+      if constexpr (kNorm) gv[v] = gr[i];
+    }
+  }
+  u32x4 w[F::kBatch][NV];
+  load_gate_round<NV>(wr, experts, 0, w);
+  float xn[NN][8];
+  if (norm_wave) {
+    float ss = 0.f;
+#pragma unroll
+    for (int v = 0; v < NN; ++v) {
+      const int i = t + v * kRouterThreads;
+      if (i >= nvec) continue;
+      unpack8(xv[v], xn[v]);
+      if constexpr (kAdd) {
+        float g[8];
+        unpack8(av[v], g);
+        u32x4 o;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) xn[v][c] = round_bf16(xn[v][c] + alpha * g[c]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = pack_bf16(xn[v][2 * c], xn[v][2 * c + 1]);
+        xr[i] = o;
+      }
+      if constexpr (kNorm) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) ss += xn[v][c] * xn[v][c];
+      } else {
+        zs[i] = xv[v];
+      }
+    }
+    if constexpr (kNorm) {
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave] = ss;
+    }
+  }
+  if constexpr (kNorm) {
+    __syncthreads();
+    if (norm_wave) {
+      float total = 0.f;
+#pragma unroll
+      for (int q = 0; q < kRouterWaves; ++q) total += red[q];
+      const float scale = 1.0f / sqrtf(total / (float)(nvec * 8) + eps);
+      u32x4 *zr = reinterpret_cast<u32x4 *>(z + row * nvec * 8);
+#pragma unroll
+      for (int v = 0; v < NN; ++v) {
+        const int i = t + v * kRouterThreads;
+        if (i >= nvec) continue;
+        float g[8];
+        unpack8(gv[v], g);
+        u32x4 o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          o[c] = pack_bf16(round_bf16(xn[v][2 * c] * scale) * g[2 * c],
+                           round_bf16(xn[v][2 * c + 1] * scale) * g[2 * c + 1]);
+        zs[i] = o;
+        zr[i] = o;
+      }
+    }
+  }
+  __syncthreads();
+  bf16 *lrow = logits_out ? logits_out + row * experts : nullptr;
+  gate_round<NV>(zs, experts, 0, w, logit, lrow);
+  for (int round = 1; round * F::kRound < experts; ++round) {
+    load_gate_round<NV>(wr, experts, round, w);
+    gate_round<NV>(zs, experts, round, w, logit, lrow);
+  }
+  __syncthreads();
+  select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
+}
+
+// hidden = 512 * NV for an instantiated NV, else 0.
+int fast_nv(int64_t hidden) {
+  if (hidden % 512) return 0;
+  const int64_t nv = hidden / 512;
+  return (nv == 1 || nv == 2 || nv == 3 || nv == 4 || nv == 6 || nv == 8) ? (int)nv : 0;
+}
+
+template <bool kNorm, bool kAdd>
+void launch_fast_router(int nv, int64_t tokens, bf16 *x, const bf16 *a, float alpha, const bf16 *nw,
+                        float eps, bf16 *z, const bf16 *wr, int experts, int topk, int renormalize,
+                        bf16 *logits_out, float *tw, int32_t *tid, hipStream_t s) {
+  const dim3 grid((unsigned)tokens);
+  switch (nv) {
+#define LM_FAST_ROUTER(NV)                                                                     \
+  case NV:                                                                                     \
+    fast_router_kernel<NV, kNorm, kAdd><<<grid, kFastThreads, 0, s>>>(                        \
+        x, a, alpha, nw, eps, z, wr, experts, topk, renormalize, logits_out, tw, tid);         \
+    break;
+    LM_FAST_ROUTER(1) LM_FAST_ROUTER(2) LM_FAST_ROUTER(3) LM_FAST_ROUTER(4) LM_FAST_ROUTER(6)
+    LM_FAST_ROUTER(8)
+#undef LM_FAST_ROUTER
+  }
+}
+
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / kWave;
 constexpr int kMaxAlignExperts = 511;
@@ -306,6 +486,14 @@ extern "C" int lm_router(const void *x, const void *gate_weight, int64_t tokens,
     return LM_EUNSUPPORTED;
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(x && gate_weight && topk_weights && topk_ids);
+  if (const int nv = fast_nv(hidden)) {
+    launch_fast_router<false, false>(nv, tokens, (bf16 *)x, nullptr, 0.f, nullptr, 0.f, nullptr,
+                                     (const bf16 *)gate_weight, (int)experts, (int)topk,
+                                     renormalize, (bf16 *)logits_out, topk_weights, topk_ids,
+                                     (hipStream_t)stream);
+    LM_CHECK_LAUNCH();
+    return LM_OK;
+  }
   router_kernel<<<dim3((unsigned)tokens), kRouterThreads, 0, (hipStream_t)stream>>>(
       (const bf16 *)x, (const bf16 *)gate_weight, (int)hidden, (int)experts, (int)topk,
       renormalize, (bf16 *)logits_out, topk_weights, topk_ids);
@@ -324,6 +512,22 @@ extern "C" int lm_add_rmsnorm_router(void *x, const void *a, float alpha, const 
     return LM_EUNSUPPORTED;
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(x && norm_weight && z && gate_weight && topk_weights && topk_ids);
+  if (const int nv = fast_nv(hidden)) {
+    if (a)
+      launch_fast_router<true, true>(nv, tokens, (bf16 *)x, (const bf16 *)a, alpha,
+                                     (const bf16 *)norm_weight, eps, (bf16 *)z,
+                                     (const bf16 *)gate_weight, (int)experts, (int)topk,
+                                     renormalize, (bf16 *)logits_out, topk_weights, topk_ids,
+                                     (hipStream_t)stream);
+    else
+      launch_fast_router<true, false>(nv, tokens, (bf16 *)x, nullptr, 0.f,
+                                      (const bf16 *)norm_weight, eps, (bf16 *)z,
+                                      (const bf16 *)gate_weight, (int)experts, (int)topk,
+                                      renormalize, (bf16 *)logits_out, topk_weights, topk_ids,
+                                      (hipStream_t)stream);
+    LM_CHECK_LAUNCH();
+    return LM_OK;
+  }
   add_norm_router_kernel<<<dim3((unsigned)tokens), kRouterThreads, 0, (hipStream_t)stream>>>(
       (bf16 *)x, (const bf16 *)a, alpha, (const bf16 *)norm_weight, eps, (bf16 *)z,
       (const bf16 *)gate_weight, (int)hidden, (int)experts, (int)topk, renormalize,

@@ -166,7 +166,8 @@ def test_rope_kv_write_stores_rotated_k_and_v(write_k):
 
 # ------------------------------------------------------------------ router --
 
-@pytest.mark.parametrize("m,h,e,k", [(16, 1024, 32, 8), (64, 1536, 40, 8), (4096, 1536, 40, 8), (7, 256, 8, 2)])
+@pytest.mark.parametrize("m,h,e,k", [(16, 1024, 32, 8), (64, 1536, 40, 8), (4096, 1536, 40, 8), (7, 256, 8, 2),
+                                      (32, 1024, 128, 8), (16, 4096, 256, 8), (9, 3072, 60, 6), (5, 1280, 40, 8)])
 @torch.inference_mode()
 def test_router_ids_bit_exact_given_logits(m, h, e, k):
     z = bf((m, h), 1.0, 10 + m)
@@ -435,10 +436,11 @@ def test_finish_add_rmsnorm_equals_unfused():
     assert torch.equal(x1, x2) and torch.equal(z1, z2)
 
 
+@pytest.mark.parametrize("h", [1536, 1280])
 @pytest.mark.parametrize("with_residual", [False, True])
 @torch.inference_mode()
-def test_add_rmsnorm_route_equals_unfused(with_residual):
-    m, h, e, k = 64, 1536, 40, 8
+def test_add_rmsnorm_route_equals_unfused(with_residual, h):
+    m, e, k = 64, 40, 8
     g = torch.Generator().manual_seed(13)
     x = torch.randn(m, h, generator=g).to(torch.bfloat16).to(DEV)
     a = torch.randn(m, h, generator=g).to(torch.bfloat16).to(DEV) if with_residual else None
