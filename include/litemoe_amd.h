@@ -125,6 +125,31 @@ int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1,
                     float scale, int64_t max_len, int64_t num_splits, void *out,
                     void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Decode attention fused with the packed QKV projection's reduction, RoPE and
+ * the KV-cache store, for one new token per row:
+ *   qkv[b] = bf16(sum_s qkv_partials[s][b])   (slices s ascending; the bf16
+ *            output of F.linear, partials from lm_linear_splitk)
+ *   q, k   = rope(qkv[b] q|k heads, positions[b])       (lm_rope_kv_write)
+ *   k_cache[b,h,p], v_cache[b,h,p] = k, v  if active[b] and 0 <= p < capacity
+ *   out    = lm_flash_decode over keys j < used[b] of the updated cache
+ * with p = positions[b]. Results are bitwise those of lm_rope_kv_write
+ * followed by lm_flash_decode; the new key is taken from registers rather
+ * than re-read. Fuses litemoe/model.py:47-71 after the projection (qkv split,
+ * `_rope`, `cache.write` -> kv_write.py:12-20, and the decode attention of
+ * flash_decode.py:16-22). qkv_partials: fp32 [qkv_splits][batch][(q_heads +
+ * 2*kv_heads) * 64] (q heads, then k, then v); 1 <= qkv_splits <= 8;
+ * cos_sin, table_len, positions, active as lm_rope_kv_write (active may be
+ * NULL: every row writes). Other arguments and the workspace as
+ * lm_flash_decode. */
+int lm_flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits,
+                        const void *cos_sin, int64_t table_len,
+                        const int64_t *positions, const uint8_t *active,
+                        void *k_cache, void *v_cache, const int32_t *used,
+                        int64_t batch, int64_t q_heads, int64_t kv_heads,
+                        int64_t capacity, int64_t head_dim, float scale,
+                        int64_t max_len, int64_t num_splits, void *out,
+                        void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Variable-length attention over a packed batch (one row per token):
  * sequence s owns tokens [cu[s], cu[s+1]); token i of it attends keys
  * [0, i] of the same sequence when causal, all of them otherwise.
@@ -249,6 +274,29 @@ int lm_moe_finish(const void *y, const int32_t *ids, const int64_t *order,
                   int64_t count, void *workspace, int64_t workspace_bytes,
                   void *stream);
 
+/* ------------------------------------------------- decode projections -- */
+
+/* Split-K projection for decode-sized row counts:
+ *   partials[s][m][n] = sum_{k in slice s} a[m][k] * weight[n][k]   (fp32)
+ * over `splits` equal K slices. bf16(sum_s partials[s]) (slices ascending) is
+ * F.linear(a, weight)'s bf16 output; lm_linear_splitk_reduce forms it, and
+ * lm_flash_decode_qkv / lm_add_rmsnorm_router_splitk consume the partials
+ * directly. Replaces the dense projections of litemoe/model.py:47-49 (packed
+ * q|k|v) and :73 (o_proj), torch F.linear in the reference. a: bf16 [rows,
+ * in_features], row stride lda (a multiple of 8); weight: bf16
+ * [out_features, in_features] contiguous. Supported: 1 <= rows <= 128,
+ * out_features % 32 == 0, in_features = splits * 128 * kw with kw in
+ * {1, 2, 3, 4, 6, 8}; otherwise LM_EUNSUPPORTED. partials: fp32
+ * [splits, rows, out_features]. */
+int lm_linear_splitk(const void *a, int64_t lda, const void *weight,
+                     int64_t rows, int64_t out_features, int64_t in_features,
+                     int64_t splits, float *partials, void *stream);
+
+/* out[m][n] = bf16(sum_s partials[s][m][n]), s ascending; out row stride ldo. */
+int lm_linear_splitk_reduce(const float *partials, int64_t splits, int64_t rows,
+                            int64_t out_features, void *out, int64_t ldo,
+                            void *stream);
+
 /* ------------------------------------------------------ fused decode ops -- */
 
 /* Residual add, RMSNorm and the router in one pass per token:
@@ -264,6 +312,22 @@ int lm_add_rmsnorm_router(void *x, const void *a, float alpha,
                           int renormalize, void *logits_out,
                           float *topk_weights, int32_t *topk_ids,
                           void *stream);
+
+/* lm_add_rmsnorm_router with the residual branch given as split-K partials
+ * (lm_linear_splitk of the attention output projection):
+ *   a[t] = bf16(sum_s a_partials[s][t]) (s ascending), then as
+ *   lm_add_rmsnorm_router. Bitwise equal to lm_linear_splitk_reduce followed
+ * by lm_add_rmsnorm_router. Fuses the o_proj output of litemoe/model.py:73
+ * into :108-113. a_partials: fp32 [a_splits][tokens][hidden], 1 <= a_splits
+ * <= 8; hidden a multiple of 512 up to 4096 (else LM_EUNSUPPORTED). */
+int lm_add_rmsnorm_router_splitk(void *x, const float *a_partials,
+                                 int64_t a_splits, float alpha,
+                                 const void *norm_weight, float eps, void *z,
+                                 const void *gate_weight, int64_t tokens,
+                                 int64_t hidden, int64_t experts, int64_t topk,
+                                 int renormalize, void *logits_out,
+                                 float *topk_weights, int32_t *topk_ids,
+                                 void *stream);
 
 /* Workspace for lm_moe_routes. */
 int lm_moe_routes_workspace_size(int64_t tokens, int64_t topk, int64_t hidden,

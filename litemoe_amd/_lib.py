@@ -46,6 +46,12 @@ _SIGNATURES = {
     "lm_moe_routes_workspace_size": [_i64, _i64, _i64, _i64, _i64, C.POINTER(C.c_int64)],
     "lm_moe_routes": [_v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v, _i64, _v],
     "lm_moe_finish_add_rmsnorm": [_v, _v, _v, _v, _v, _f32, _v, _f32, _v, _i64, _i64, _i64, _v],
+    "lm_linear_splitk": [_v, _i64, _v, _i64, _i64, _i64, _i64, _v, _v],
+    "lm_linear_splitk_reduce": [_v, _i64, _i64, _i64, _v, _i64, _v],
+    "lm_flash_decode_qkv": [_v, _i64, _v, _i64, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64,
+                            _f32, _i64, _i64, _v, _v, _i64, _v],
+    "lm_add_rmsnorm_router_splitk": [_v, _v, _i64, _f32, _v, _f32, _v, _v, _i64, _i64, _i64, _i64,
+                                     _i32, _v, _v, _v, _v],
 }
 _RESTYPE = {"lm_version": C.c_char_p, "lm_status_string": C.c_char_p}
 

@@ -39,40 +39,80 @@ __device__ __forceinline__ float merge_factor(float m, float mnew) {
   return m == -INFINITY ? 0.f : __expf(m - mnew);
 }
 
-template <int G>
-__global__ void __launch_bounds__(kThreads)
-decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 *__restrict__ kc,
-              const bf16 *__restrict__ vc, const int32_t *__restrict__ used, int q_heads,
+// The projection-fused form (lm_flash_decode_qkv): q, k and v of the row
+// come from the split-K partials of the packed QKV projection instead of a
+// rotated q and a cache that already holds the new key.
+struct QkvIn {
+  const float *part;      // [splits][batch][(q_heads + 2*kv_heads) * 64], NULL: unfused
+  int splits;
+  const bf16 *cos_sin;    // [table_len, 64]: cos | sin halves
+  int64_t table_len;
+  const int64_t *pos;     // [batch] position of the new key
+  const uint8_t *active;  // [batch] or NULL (all rows write)
+};
+
+constexpr int kMaxQkvSplits = 8;
+
+// Neox rotation of one (x1, x2) pair with the reference's three roundings
+// (the arithmetic of rope_kv_kernel).
+__device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s, float &o1,
+                                            float &o2) {
+  o1 = round_bf16(round_bf16(x1 * c) - round_bf16(x2 * s));
+  o2 = round_bf16(round_bf16(x2 * c) + round_bf16(x1 * s));
+}
+
+// G <= 3: four waves per SIMD (two workgroups per CU, <= 128 VGPRs); the KV stream
+// needs both workgroups in flight.
+template <int G, bool kFused>
+__global__ void __launch_bounds__(kThreads, G <= 3 ? 4 : 2)
+decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__restrict__ kc,
+              bf16 *__restrict__ vc, const int32_t *__restrict__ used, int q_heads,
               int kv_heads, int64_t capacity, float scale, int max_len, int chunk, int splits,
-              Partial part, bf16 *__restrict__ out) {
+              Partial part, QkvIn in, bf16 *__restrict__ out) {
   __shared__ float sm_o[kWaves][G][kD];
   __shared__ float sm_m[kWaves][G];
   __shared__ float sm_l[kWaves][G];
+  __shared__ float sm_qkv[kFused ? G + 2 : 1][kD];
+  __shared__ float sm_knew[kFused ? kD : 1];
   const int split = blockIdx.x, h = blockIdx.y;
   const int64_t b = blockIdx.z;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int ks = lane / kLanesPerKey, dc = lane % kLanesPerKey;
+  // Fused: this row's q|k|v slices of the packed projection, summed over the
+  // K slices in ascending order and rounded to bf16 (F.linear's output);
+  // the loads are issued before anything waits.
+  f32x4 pv[kMaxQkvSplits];
+  const int nstage = (G + 2) * (kD / 4);  // threads staging 4 channels each
+  int64_t pnew = 0;
+  if constexpr (kFused) {
+    pnew = in.pos[b];
+    if (threadIdx.x < nstage) {
+      const int hs = threadIdx.x / (kD / 4), c4 = (threadIdx.x % (kD / 4)) * 4;
+      const int head = hs < G ? h * G + hs : (hs == G ? q_heads + h : q_heads + kv_heads + h);
+      const int64_t ncols = (int64_t)(q_heads + 2 * kv_heads) * kD;
+      const float *src = in.part + b * ncols + (int64_t)head * kD + c4;
+#pragma unroll
+      for (int s = 0; s < kMaxQkvSplits; ++s)
+        if (s < in.splits)
+          pv[s] = *reinterpret_cast<const f32x4 *>(src + (int64_t)s * gridDim.z * ncols);
+    }
+  }
   int n = used[b];
   n = min(n, max_len);
   n = (int)min((int64_t)n, capacity);
   const int k0 = split * chunk;
   const int k1 = min(n, k0 + chunk);
-  if (splits > 1 && k0 >= n) return;  // the combine kernel skips empty splits
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int ks = lane / kLanesPerKey, dc = lane % kLanesPerKey;
-  float qv[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const bf16 *qp = q + b * qs0 + (int64_t)(h * G + g) * qs1 + dc * 8;
-    unpack8(*reinterpret_cast<const u32x4 *>(qp), qv[g]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qv[g][i] *= scale;
-  }
-  float m[G], l[G], acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+  if (splits > 1 && k0 >= n && !kFused) return;  // the combine kernel skips empty splits
+  // The new key is stored by the split whose key range holds its position
+  // (split 0 when none does) and, when attended, taken from registers there:
+  // its cache slot is loaded with the others but replaced.
+  bool writer = false, own = false;
+  if constexpr (kFused) {
+    const bool writes = (!in.active || in.active[b]) && pnew >= 0 && pnew < capacity;
+    const int64_t wsplit = pnew >= 0 && pnew < (int64_t)gridDim.x * chunk ? pnew / chunk : 0;
+    writer = writes && split == wsplit;
+    own = writer && pnew >= k0 && pnew < k1;
+    if (splits > 1 && k0 >= n && !writer) return;
   }
   const int64_t head_base = ((int64_t)b * kv_heads + h) * capacity * kD + dc * 8;
   const bf16 *kbase = kc + head_base;
@@ -88,13 +128,107 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 *
       vb[u] = *reinterpret_cast<const u32x4 *>(vbase + (int64_t)j * kD);
     }
   };
+  // Loads complete in issue order: the rotation table row goes first, then
+  // the first two KV iterations, so nothing below waits on the KV stream.
+  const bool in_table = kFused && pnew >= 0 && pnew < in.table_len;
+  const int c0 = 8 * (dc % 4);
+  u32x4 cs_c, cs_s;
+  if constexpr (kFused) {
+    const bf16 *cs = in.cos_sin + (in_table ? pnew : 0) * kD;
+    cs_c = *reinterpret_cast<const u32x4 *>(cs + c0);
+    cs_s = *reinterpret_cast<const u32x4 *>(cs + kD / 2 + c0);
+  }
+  u32x4 ka[kU], va[kU], kb2[kU], vb2[kU];
+  if (niter > 0) load(ka, va, 0);
+  if (niter > 1) load(kb2, vb2, 1);
+
+  float qv[G][8];
+  if constexpr (kFused) {
+    float cf[8], sf[8];
+    unpack8(cs_c, cf);
+    unpack8(cs_s, sf);
+    if (threadIdx.x < nstage) {
+      const int hs = threadIdx.x / (kD / 4), c4 = (threadIdx.x % (kD / 4)) * 4;
+      f32x4 acc4 = pv[0];
+#pragma unroll
+      for (int s = 1; s < kMaxQkvSplits; ++s)
+        if (s < in.splits) acc4 += pv[s];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm_qkv[hs][c4 + i] = round_bf16(acc4[i]);
+    }
+    __syncthreads();
+    // Rotate the (x1, x2) halves of head slot hs; lane dc keeps its half.
+    auto rotated = [&](int hs, float *o) {
+      float r1[8], r2[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float x1 = sm_qkv[hs][c0 + i], x2 = sm_qkv[hs][kD / 2 + c0 + i];
+        if (in_table) {
+          rotate_pair(x1, x2, cf[i], sf[i], r1[i], r2[i]);
+        } else {
+          r1[i] = x1;
+          r2[i] = x2;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = dc < 4 ? r1[i] : r2[i];
+    };
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      rotated(g, qv[g]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qv[g][i] *= scale;
+    }
+    // The rotated new key goes to LDS (for the substitution) and, with the
+    // value, to the cache.
+    if (writer && wave == 0 && ks == 0) {
+      float knew[8];
+      rotated(G, knew);
+      const int64_t at = (((int64_t)b * kv_heads + h) * capacity + pnew) * kD + dc * 8;
+      u32x4 ko, vo;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm_knew[dc * 8 + i] = knew[i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ko[i] = pack_bf16(knew[2 * i], knew[2 * i + 1]);
+        vo[i] = pack_bf16(sm_qkv[G + 1][dc * 8 + 2 * i], sm_qkv[G + 1][dc * 8 + 2 * i + 1]);
+      }
+      *reinterpret_cast<u32x4 *>(kc + at) = ko;
+      *reinterpret_cast<u32x4 *>(vc + at) = vo;
+    }
+    if (own) __syncthreads();  // uniform across the workgroup
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const bf16 *qp = q + b * qs0 + (int64_t)(h * G + g) * qs1 + dc * 8;
+      unpack8(*reinterpret_cast<const u32x4 *>(qp), qv[g]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qv[g][i] *= scale;
+    }
+  }
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+  }
+
   auto compute = [&](const u32x4 *kb, const u32x4 *vb, int it) {
     float s[kU][G];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const bool ok = first + it * kKeysPerIter + u * kSlots < k1;
+      const int j = first + it * kKeysPerIter + u * kSlots;
+      const bool ok = j < k1;
       float kf[8];
       unpack8(kb[u], kf);
+      if constexpr (kFused) {
+        if (own && j == pnew) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) kf[i] = sm_knew[dc * 8 + i];
+        }
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float d = 0.f;
@@ -106,7 +240,15 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 *
     }
     float vf[kU][8];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) unpack8(vb[u], vf[u]);
+    for (int u = 0; u < kU; ++u) {
+      unpack8(vb[u], vf[u]);
+      if constexpr (kFused) {
+        if (own && first + it * kKeysPerIter + u * kSlots == pnew) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) vf[u][i] = sm_qkv[G + 1][dc * 8 + i];
+        }
+      }
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float mx = m[g];
@@ -128,13 +270,14 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 *
     }
   };
 
-  u32x4 ka[kU], va[kU], kb2[kU], vb2[kU];
-  if (niter > 0) load(ka, va, 0);
+  // Two iterations in flight: iteration it+2 is issued once it is consumed.
   for (int it = 0; it < niter; it += 2) {
-    if (it + 1 < niter) load(kb2, vb2, it + 1);
     compute(ka, va, it);
     if (it + 2 < niter) load(ka, va, it + 2);
-    if (it + 1 < niter) compute(kb2, vb2, it + 1);
+    if (it + 1 < niter) {
+      compute(kb2, vb2, it + 1);
+      if (it + 3 < niter) load(kb2, vb2, it + 3);
+    }
   }
 
   // Merge the 8 key slots of the wave (lanes with equal dc).
@@ -233,17 +376,14 @@ extern "C" int lm_flash_decode_workspace_size(int64_t batch, int64_t q_heads, in
   return LM_OK;
 }
 
-extern "C" int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1, const void *k_cache,
-                               const void *v_cache, const int32_t *used, int64_t batch,
-                               int64_t q_heads, int64_t kv_heads, int64_t capacity,
-                               int64_t head_dim, float scale, int64_t max_len, int64_t num_splits,
-                               void *out, void *workspace, int64_t workspace_bytes_, void *stream) {
-  LM_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 &&
-             capacity > 0 && max_len > 0 && num_splits > 0 && num_splits <= 1024 &&
-             max_len < ((int64_t)1 << 30));
-  if (head_dim != kD) return LM_EUNSUPPORTED;
-  if (batch == 0) return LM_OK;
-  LM_REQUIRE(q && k_cache && v_cache && used && out);
+namespace {
+
+// Shared launcher of lm_flash_decode and lm_flash_decode_qkv.
+int launch_decode(const void *q, int64_t qs0, int64_t qs1, void *k_cache, void *v_cache,
+                  const int32_t *used, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                  int64_t capacity, float scale, int64_t max_len, int64_t num_splits,
+                  const QkvIn &in, void *out, void *workspace, int64_t workspace_bytes_,
+                  void *stream) {
   const int64_t need = workspace_bytes(batch, q_heads, num_splits);
   if (need > 0 && (!workspace || workspace_bytes_ < need)) return LM_EWORKSPACE;
   const int chunk = (int)align_up(cdiv(max_len, num_splits), 16);
@@ -251,23 +391,30 @@ extern "C" int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1, const vo
   Partial part{nullptr, nullptr, nullptr};
   if (splits > 1) {
     const int64_t n = batch * q_heads * num_splits;
-    char *p = static_cast<char *>(workspace);
-    part.o = reinterpret_cast<float *>(p);
-    part.m = reinterpret_cast<float *>(p + n * kD * 4);
-    part.l = reinterpret_cast<float *>(p + n * kD * 4 + (n * 4 + 255) / 256 * 256);
+    char *w = static_cast<char *>(workspace);
+    part.o = reinterpret_cast<float *>(w);
+    part.m = reinterpret_cast<float *>(w + n * kD * 4);
+    part.l = reinterpret_cast<float *>(w + n * kD * 4 + (n * 4 + 255) / 256 * 256);
   }
   // Partials are indexed with the caller's split count as the stride.
   const int stride_splits = splits > 1 ? (int)num_splits : 1;
   const dim3 grid((unsigned)splits, (unsigned)kv_heads, (unsigned)batch);
   hipStream_t s = (hipStream_t)stream;
   const int G = (int)(q_heads / kv_heads);
+  const bool fused = in.part != nullptr;
   switch (G) {
-#define X(GG)                                                                                   \
-  case GG:                                                                                      \
-    decode_kernel<GG><<<grid, kThreads, 0, s>>>((const bf16 *)q, qs0, qs1, (const bf16 *)k_cache, \
-                                                 (const bf16 *)v_cache, used, (int)q_heads,       \
-                                                 (int)kv_heads, capacity, scale, (int)max_len,     \
-                                                 chunk, stride_splits, part, (bf16 *)out);         \
+#define X(GG)                                                                                     \
+  case GG:                                                                                        \
+    if (fused)                                                                                    \
+      decode_kernel<GG, true><<<grid, kThreads, 0, s>>>(                                          \
+          (const bf16 *)q, qs0, qs1, (bf16 *)k_cache, (bf16 *)v_cache, used, (int)q_heads,        \
+          (int)kv_heads, capacity, scale, (int)max_len, chunk, stride_splits, part, in,           \
+          (bf16 *)out);                                                                           \
+    else                                                                                          \
+      decode_kernel<GG, false><<<grid, kThreads, 0, s>>>(                                         \
+          (const bf16 *)q, qs0, qs1, (bf16 *)k_cache, (bf16 *)v_cache, used, (int)q_heads,        \
+          (int)kv_heads, capacity, scale, (int)max_len, chunk, stride_splits, part, in,           \
+          (bf16 *)out);                                                                           \
     break;
     X(1) X(2) X(3) X(4) X(6) X(8)
 #undef X
@@ -281,4 +428,47 @@ extern "C" int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1, const vo
     LM_CHECK_LAUNCH();
   }
   return LM_OK;
+}
+
+bool decode_args_ok(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
+                    int64_t max_len, int64_t num_splits) {
+  return batch >= 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && capacity > 0 &&
+         max_len > 0 && num_splits > 0 && num_splits <= 1024 && max_len < ((int64_t)1 << 30) &&
+         batch <= 65535 && kv_heads <= 65535;
+}
+
+}  // namespace
+
+extern "C" int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1, const void *k_cache,
+                               const void *v_cache, const int32_t *used, int64_t batch,
+                               int64_t q_heads, int64_t kv_heads, int64_t capacity,
+                               int64_t head_dim, float scale, int64_t max_len, int64_t num_splits,
+                               void *out, void *workspace, int64_t workspace_bytes_, void *stream) {
+  LM_REQUIRE(decode_args_ok(batch, q_heads, kv_heads, capacity, max_len, num_splits));
+  if (head_dim != kD) return LM_EUNSUPPORTED;
+  if (batch == 0) return LM_OK;
+  LM_REQUIRE(q && k_cache && v_cache && used && out);
+  const QkvIn in{nullptr, 0, nullptr, 0, nullptr, nullptr};
+  return launch_decode(q, qs0, qs1, const_cast<void *>(k_cache), const_cast<void *>(v_cache),
+                       used, batch, q_heads, kv_heads, capacity, scale, max_len, num_splits, in,
+                       out, workspace, workspace_bytes_, stream);
+}
+
+extern "C" int lm_flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits,
+                                   const void *cos_sin, int64_t table_len,
+                                   const int64_t *positions, const uint8_t *active,
+                                   void *k_cache, void *v_cache, const int32_t *used,
+                                   int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                   int64_t capacity, int64_t head_dim, float scale,
+                                   int64_t max_len, int64_t num_splits, void *out,
+                                   void *workspace, int64_t workspace_bytes_, void *stream) {
+  LM_REQUIRE(decode_args_ok(batch, q_heads, kv_heads, capacity, max_len, num_splits));
+  LM_REQUIRE(qkv_splits >= 1 && table_len > 0);
+  if (head_dim != kD || qkv_splits > kMaxQkvSplits) return LM_EUNSUPPORTED;
+  if (batch == 0) return LM_OK;
+  LM_REQUIRE(qkv_partials && cos_sin && positions && k_cache && v_cache && used && out);
+  const QkvIn in{qkv_partials, (int)qkv_splits, (const bf16 *)cos_sin, table_len, positions,
+                 active};
+  return launch_decode(nullptr, 0, 0, k_cache, v_cache, used, batch, q_heads, kv_heads, capacity,
+                       scale, max_len, num_splits, in, out, workspace, workspace_bytes_, stream);
 }

@@ -1,0 +1,155 @@
+// Split-K dense projection for decode-sized row counts on MFMA:
+//
+//   partials[s][m][n] = sum_{k in slice s} A[m][k] * W[n][k]        (fp32)
+//
+// W is an nn.Linear weight [N, K] (row-major), A is bf16 [M, K] with row
+// stride lda, M <= 128. F.linear's bf16 output is bf16(sum_s partials[s]),
+// the slices summed in ascending order; lm_linear_splitk_reduce does that,
+// and the decode consumers (lm_flash_decode_qkv, lm_add_rmsnorm_router_splitk)
+// do it on their own loads, so the projection costs one launch and the
+// reduction none.
+//
+// Why split K: with M = batch rows, every workgroup that covers the full K
+// range must read all of A (M x K bf16), which bounds the workgroup by its
+// CU's load rate rather than by HBM. Slicing K divides both A and W per
+// workgroup; the price is S fp32 partial rows, read once by the consumer.
+//
+// Workgroup (column tile of 32, slice s), 4 waves; wave w takes KW 32-wide
+// k steps of the slice. Each wave loads its B fragment (32 weight rows) and
+// the A fragments of every 16-row block once, all before any MFMA; the four
+// wave partials are summed through LDS in a fixed order.
+//
+// Reference: the projections of litemoe/model.py:47-49 (qkv) and :73 (o_proj),
+// F.linear in the reference.
+#include "internal.h"
+
+namespace lm {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kTileN = 32;
+constexpr int kMaxRows = 128;
+
+__device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+template <int KW, int MB>
+__global__ void __launch_bounds__(kThreads)
+splitk_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w, int M, int N,
+              int K, float *__restrict__ part) {
+  __shared__ float red[kWaves][MB][2][4][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int col = lane % 16, grp = lane / 16;
+  const int n0 = blockIdx.x * kTileN, s = blockIdx.y;
+  const int k0 = (s * kWaves + wave) * KW * 32 + grp * 8;
+  u32x4 b[2][KW], av[MB][KW];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const bf16 *wr = w + (int64_t)(n0 + 16 * j + col) * K + k0;
+#pragma unroll
+    for (int t = 0; t < KW; ++t) b[j][t] = load16(wr + t * 32);
+  }
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    const bf16 *ar = a + (int64_t)min(m * 16 + col, M - 1) * lda + k0;
+#pragma unroll
+    for (int t = 0; t < KW; ++t) av[m][t] = load16(ar + t * 32);
+  }
+  f32x4 c[MB][2];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) c[m][0] = c[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < KW; ++t)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      c[m][0] = mfma16x16x32(av[m][t], b[0][t], c[m][0]);
+      c[m][1] = mfma16x16x32(av[m][t], b[1][t], c[m][1]);
+    }
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][m][j][i][lane] = c[m][j][i];
+  __syncthreads();
+  // Thread -> (row, column) of the MB*16 x 32 tile; C row r of a 16x16 block
+  // is held by lanes 16*(r/4) .. +15 at index r%4.
+  for (int o = threadIdx.x; o < MB * 16 * kTileN; o += kThreads) {
+    const int row = o / kTileN, cc = o % kTileN;
+    if (row >= M) break;
+    const int m = row / 16, r = row % 16, j = cc / 16;
+    const int l = cc % 16 + 16 * (r / 4), i = r % 4;
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < kWaves; ++q) v += red[q][m][j][i][l];
+    part[((int64_t)s * M + row) * N + n0 + cc] = v;
+  }
+}
+
+// out[m][n] = bf16(sum_s partials[s][m][n]), slices in ascending order.
+__global__ void __launch_bounds__(256)
+splitk_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
+                     bf16 *__restrict__ out, int64_t ldo) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * N) return;
+  const int64_t m = idx / N, n = idx % N;
+  float v = 0.f;
+  for (int s = 0; s < splits; ++s) v += part[(int64_t)s * M * N + idx];
+  out[m * ldo + n] = (bf16)f32_to_bf16(v);
+}
+
+int row_blocks(int64_t M) {
+  const int64_t mb = cdiv(M, 16);
+  return mb <= 1 ? 1 : mb <= 2 ? 2 : mb <= 4 ? 4 : 8;
+}
+
+}  // namespace
+
+bool splitk_shape_ok(int64_t M, int64_t N, int64_t K, int64_t splits) {
+  if (M < 1 || M > kMaxRows || N % kTileN || splits < 1 || K % (splits * kWaves * 32)) return false;
+  const int64_t kw = K / (splits * kWaves * 32);
+  return kw == 1 || kw == 2 || kw == 3 || kw == 4 || kw == 6 || kw == 8;
+}
+
+}  // namespace lm
+
+using namespace lm;
+
+extern "C" int lm_linear_splitk(const void *a, int64_t lda, const void *weight, int64_t rows,
+                                int64_t out_features, int64_t in_features, int64_t splits,
+                                float *partials, void *stream) {
+  LM_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0 && splits > 0 &&
+             lda >= in_features && lda % 8 == 0);
+  if (rows == 0) return LM_OK;
+  if (!splitk_shape_ok(rows, out_features, in_features, splits)) return LM_EUNSUPPORTED;
+  LM_REQUIRE(a && weight && partials);
+  const int kw = (int)(in_features / (splits * kWaves * 32));
+  const dim3 grid((unsigned)(out_features / kTileN), (unsigned)splits);
+  hipStream_t s = (hipStream_t)stream;
+  const int M = (int)rows, N = (int)out_features, K = (int)in_features;
+  const int mb = row_blocks(rows);
+#define LM_SPLITK(KW, MB)                                                                         \
+  if (kw == KW && mb == MB) {                                                                     \
+    splitk_kernel<KW, MB><<<grid, kThreads, 0, s>>>((const bf16 *)a, lda, (const bf16 *)weight, M, \
+                                                    N, K, partials);                              \
+    LM_CHECK_LAUNCH();                                                                            \
+    return LM_OK;                                                                                 \
+  }
+#define LM_SPLITK_MB(KW) LM_SPLITK(KW, 1) LM_SPLITK(KW, 2) LM_SPLITK(KW, 4) LM_SPLITK(KW, 8)
+  LM_SPLITK_MB(1) LM_SPLITK_MB(2) LM_SPLITK_MB(3) LM_SPLITK_MB(4) LM_SPLITK_MB(6) LM_SPLITK_MB(8)
+#undef LM_SPLITK_MB
+#undef LM_SPLITK
+  return LM_EUNSUPPORTED;
+}
+
+extern "C" int lm_linear_splitk_reduce(const float *partials, int64_t splits, int64_t rows,
+                                       int64_t out_features, void *out, int64_t ldo, void *stream) {
+  LM_REQUIRE(splits > 0 && rows >= 0 && out_features > 0 && ldo >= out_features);
+  if (rows == 0) return LM_OK;
+  LM_REQUIRE(partials && out);
+  const int64_t n = rows * out_features;
+  splitk_reduce_kernel<<<dim3((unsigned)cdiv(n, 256)), 256, 0, (hipStream_t)stream>>>(
+      partials, (int)splits, (int)rows, (int)out_features, (bf16 *)out, ldo);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}

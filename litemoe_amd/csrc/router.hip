@@ -254,15 +254,18 @@ __device__ __forceinline__ void gate_round(const u32x4 *zs, int experts, int rou
   }
 }
 
+constexpr int kMaxResidualSplits = 8;
+
 // kNorm: z = rmsnorm(x [+ alpha*a]) is routed (and x, z are written);
-// otherwise x itself is routed.
-template <int NV, bool kNorm, bool kAdd>
+// otherwise x itself is routed. kPart: a is given as fp32 split-K partials
+// [asplits][tokens][hidden] (lm_linear_splitk) and a = bf16(sum of slices).
+template <int NV, bool kNorm, bool kAdd, bool kPart>
 __global__ void __launch_bounds__(kFastThreads)
 fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha,
                    const bf16 *__restrict__ nw, float eps, bf16 *__restrict__ z,
                    const bf16 *__restrict__ wr, int experts, int topk, int renormalize,
                    bf16 *__restrict__ logits_out, float *__restrict__ tw,
-                   int32_t *__restrict__ tid) {
+                   int32_t *__restrict__ tid, const float *__restrict__ ap, int asplits) {
   typedef FastRouter<NV> F;
   constexpr int nvec = F::kNvec, NN = F::kNorm;
   __shared__ u32x4 zs[nvec];
@@ -277,12 +280,23 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
   const u32x4 *ar = reinterpret_cast<const u32x4 *>(a + row * nvec * 8);
   const u32x4 *gr = reinterpret_cast<const u32x4 *>(nw);
   u32x4 xv[NN], av[NN], gv[NN];
+  f32x4 pv[kPart ? NN : 1][kPart ? kMaxResidualSplits : 1][2];
   if (norm_wave) {
 #pragma unroll
     for (int v = 0; v < NN; ++v) {
       const int i = min(t + v * kRouterThreads, nvec - 1);
       xv[v] = xr[i];
-      if constexpr (kAdd) av[v] = ar[i];
+      if constexpr (kPart) {
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(ap + row * nvec * 8) + 2 * i;
+#pragma unroll
+        for (int s = 0; s < kMaxResidualSplits; ++s)
+          if (s < asplits) {
+            pv[v][s][0] = src[(int64_t)s * gridDim.x * nvec * 2];
+            pv[v][s][1] = src[(int64_t)s * gridDim.x * nvec * 2 + 1];
+          }
+      } else if constexpr (kAdd) {
+        av[v] = ar[i];
+      }
       if constexpr (kNorm) gv[v] = gr[i];
     }
   }
@@ -298,7 +312,22 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
       unpack8(xv[v], xn[v]);
       if constexpr (kAdd) {
         float g[8];
-        unpack8(av[v], g);
+        if constexpr (kPart) {
+          f32x4 lo = pv[v][0][0], hi = pv[v][0][1];
+#pragma unroll
+          for (int s = 1; s < kMaxResidualSplits; ++s)
+            if (s < asplits) {
+              lo += pv[v][s][0];
+              hi += pv[v][s][1];
+            }
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            g[c] = round_bf16(lo[c]);
+            g[4 + c] = round_bf16(hi[c]);
+          }
+        } else {
+          unpack8(av[v], g);
+        }
         u32x4 o;
 #pragma unroll
         for (int c = 0; c < 8; ++c) xn[v][c] = round_bf16(xn[v][c] + alpha * g[c]);
@@ -360,16 +389,18 @@ int fast_nv(int64_t hidden) {
   return (nv == 1 || nv == 2 || nv == 3 || nv == 4 || nv == 6 || nv == 8) ? (int)nv : 0;
 }
 
-template <bool kNorm, bool kAdd>
+template <bool kNorm, bool kAdd, bool kPart = false>
 void launch_fast_router(int nv, int64_t tokens, bf16 *x, const bf16 *a, float alpha, const bf16 *nw,
                         float eps, bf16 *z, const bf16 *wr, int experts, int topk, int renormalize,
-                        bf16 *logits_out, float *tw, int32_t *tid, hipStream_t s) {
+                        bf16 *logits_out, float *tw, int32_t *tid, hipStream_t s,
+                        const float *ap = nullptr, int asplits = 0) {
   const dim3 grid((unsigned)tokens);
   switch (nv) {
 #define LM_FAST_ROUTER(NV)                                                                     \
   case NV:                                                                                     \
-    fast_router_kernel<NV, kNorm, kAdd><<<grid, kFastThreads, 0, s>>>(                        \
-        x, a, alpha, nw, eps, z, wr, experts, topk, renormalize, logits_out, tw, tid);         \
+    fast_router_kernel<NV, kNorm, kAdd, kPart><<<grid, kFastThreads, 0, s>>>(                 \
+        x, a, alpha, nw, eps, z, wr, experts, topk, renormalize, logits_out, tw, tid, ap,      \
+        asplits);                                                                              \
     break;
     LM_FAST_ROUTER(1) LM_FAST_ROUTER(2) LM_FAST_ROUTER(3) LM_FAST_ROUTER(4) LM_FAST_ROUTER(6)
     LM_FAST_ROUTER(8)
@@ -532,6 +563,29 @@ extern "C" int lm_add_rmsnorm_router(void *x, const void *a, float alpha, const 
       (bf16 *)x, (const bf16 *)a, alpha, (const bf16 *)norm_weight, eps, (bf16 *)z,
       (const bf16 *)gate_weight, (int)hidden, (int)experts, (int)topk, renormalize,
       (bf16 *)logits_out, topk_weights, topk_ids);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+extern "C" int lm_add_rmsnorm_router_splitk(void *x, const float *a_partials, int64_t a_splits,
+                                            float alpha, const void *norm_weight, float eps,
+                                            void *z, const void *gate_weight, int64_t tokens,
+                                            int64_t hidden, int64_t experts, int64_t topk,
+                                            int renormalize, void *logits_out,
+                                            float *topk_weights, int32_t *topk_ids,
+                                            void *stream) {
+  LM_REQUIRE(tokens >= 0 && hidden > 0 && experts > 0 && topk > 0 && a_splits > 0);
+  const int nv = fast_nv(hidden);
+  if (!nv || experts > kMaxExperts || topk > kMaxTopk || topk > experts ||
+      a_splits > kMaxResidualSplits)
+    return LM_EUNSUPPORTED;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(x && a_partials && norm_weight && z && gate_weight && topk_weights && topk_ids);
+  launch_fast_router<true, true, true>(nv, tokens, (bf16 *)x, nullptr, alpha,
+                                       (const bf16 *)norm_weight, eps, (bf16 *)z,
+                                       (const bf16 *)gate_weight, (int)experts, (int)topk,
+                                       renormalize, (bf16 *)logits_out, topk_weights, topk_ids,
+                                       (hipStream_t)stream, a_partials, (int)a_splits);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

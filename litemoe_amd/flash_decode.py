@@ -5,6 +5,11 @@ Mirrors ``FlashDecode`` of litemoe/flash_decode.py:5-34: built once per
 layer caches ``k, v [B, Hkv, C, D]``; row b attends keys ``j < used[b]``
 (``used = where(active, lengths + 1, 1)`` unless given). The split count is
 fixed at construction, so the launch is capturable.
+
+``fused_qkv`` is the decode layer's form: it takes the packed QKV
+projection as split-K partials and applies the reduction, RoPE and the
+KV-cache store of the new token itself (``lm_flash_decode_qkv``), bitwise
+equal to rope_kv_write followed by ``__call__``.
 """
 import math
 
@@ -54,4 +59,34 @@ class FlashDecode:
                   used.data_ptr(), b, hq, k.shape[1], self.capacity, d, float(scale), self.maximum,
                   self.splits, out.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(),
                   _lib.stream(q.device))
+        return out
+
+    def fused_qkv(self, partials, cos_sin, positions, active, k, v, scale, used, q_heads):
+        """Attention of one new token per row from the packed QKV projection's
+        partials ``[S, B, (Hq + 2 Hkv) * 64]`` (litemoe/model.py:47-71 after
+        the projection). Writes the rotated key and the value at
+        ``positions[b]`` of ``k``/``v`` (rows with ``active`` false, when
+        given, write nothing) and returns ``[B, Hq, 1, 64]``."""
+        splits, b, ncols = partials.shape
+        hkv = k.shape[1]
+        if ncols != (q_heads + 2 * hkv) * 64 or q_heads % hkv or k.shape != v.shape:
+            raise ValueError("QKV partials do not match the cache heads")
+        if b > self.batch or k.shape[0] < b or k.shape[2] != self.capacity or k.shape[3] != 64:
+            raise ValueError("Decode attention built for another batch/capacity")
+        _lib.require_cuda(partials, k, v, positions, used, what="decode attention tensors")
+        if partials.dtype != torch.float32 or not partials.is_contiguous():
+            raise ValueError("QKV partials must be contiguous fp32")
+        if not k.is_contiguous() or not v.is_contiguous() or k.dtype != torch.bfloat16:
+            raise ValueError("Decode attention needs contiguous BF16 cache layers")
+        positions = positions.to(torch.int64).contiguous()
+        used = used.to(torch.int32).contiguous()
+        act = None
+        if active is not None:
+            # a bool mask is one byte per row: read it in place (no conversion launch)
+            act = (active.view(torch.uint8) if active.dtype == torch.bool else active.to(torch.uint8)).contiguous()
+        out = torch.empty(b, q_heads, 1, 64, device=k.device, dtype=k.dtype)
+        _lib.call("lm_flash_decode_qkv", partials.data_ptr(), splits, cos_sin.data_ptr(), cos_sin.shape[0],
+                  positions.data_ptr(), _lib.ptr(act), k.data_ptr(), v.data_ptr(), used.data_ptr(), b,
+                  q_heads, hkv, self.capacity, 64, float(scale), self.maximum, self.splits,
+                  out.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(), _lib.stream(k.device))
         return out

@@ -1,0 +1,69 @@
+"""Split-K projections for decode-sized row counts.
+
+The dense projections of the reference layer (packed q|k|v,
+litemoe/model.py:47-49, and o_proj, :73) are ``F.linear`` calls. For a decode
+batch (rows <= 128) they are computed by ``lm_linear_splitk`` as fp32
+partial sums over K slices; ``bf16(sum of slices)`` is F.linear's bf16
+output. The decode layer hands the partials straight to the consumer kernel
+(``FlashDecode.fused_qkv``, ``router.add_rmsnorm_route_splitk``), which sums
+them on load; :func:`linear` is the stand-alone form (projection + reduce).
+"""
+import torch
+
+from . import _lib
+
+MAX_ROWS = 128
+MAX_CONSUMER_SPLITS = 8
+_KW = (1, 2, 3, 4, 6, 8)
+
+
+def pick_splits(rows, out_features, in_features, target_workgroups=192, max_splits=MAX_CONSUMER_SPLITS):
+    """Fewest K slices giving about ``target_workgroups`` workgroups
+    (out_features / 32 column tiles per slice), or None when the shape has no
+    kernel. Slices are K / (128 * kw) for the compiled kw values."""
+    if not 1 <= rows <= MAX_ROWS or out_features % 32 or in_features % 128:
+        return None
+    steps = in_features // 128
+    valid = [s for s in range(1, max_splits + 1) if steps % s == 0 and steps // s in _KW]
+    if not valid:
+        return None
+    for s in valid:
+        if (out_features // 32) * s >= target_workgroups:
+            return s
+    return valid[-1]
+
+
+def linear_splitk(a, weight, splits, out=None):
+    """fp32 partials ``[splits, rows, out_features]`` of ``a @ weight.T``."""
+    _lib.require_cuda(a, weight, what="projection operands")
+    if a.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("Split-K projection supports BF16 operands")
+    if a.dim() != 2 or a.stride(1) != 1 or not weight.is_contiguous() or weight.shape[1] != a.shape[1]:
+        raise ValueError("Split-K projection needs a [rows, K] input with contiguous rows and a contiguous [N, K] weight")
+    rows, k = a.shape
+    n = weight.shape[0]
+    if out is None:
+        out = torch.empty(splits, rows, n, device=a.device, dtype=torch.float32)
+    elif out.shape != (splits, rows, n) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("Partials buffer must be contiguous fp32 [splits, rows, out_features]")
+    _lib.call("lm_linear_splitk", a.data_ptr(), a.stride(0), weight.data_ptr(), rows, n, k, splits,
+              out.data_ptr(), _lib.stream(a.device))
+    return out
+
+
+def reduce(partials, out=None):
+    """``bf16(sum over slices)``, slices in ascending order."""
+    splits, rows, n = partials.shape
+    if out is None:
+        out = torch.empty(rows, n, device=partials.device, dtype=torch.bfloat16)
+    _lib.call("lm_linear_splitk_reduce", partials.data_ptr(), splits, rows, n, out.data_ptr(),
+              out.stride(0), _lib.stream(partials.device))
+    return out
+
+
+def linear(a, weight, splits=None):
+    """``F.linear(a, weight)`` for decode-sized ``a`` (bf16, no bias)."""
+    splits = splits or pick_splits(a.shape[0], weight.shape[0], weight.shape[1])
+    if splits is None:
+        raise ValueError(f"No split-K kernel for rows={a.shape[0]}, weight {tuple(weight.shape)}")
+    return reduce(linear_splitk(a, weight, splits))

@@ -18,8 +18,12 @@ the library's experts, identity placement and no masked rows (lean decode,
 packed prefill) the layer tail is fused further into three launches:
 ``lm_add_rmsnorm_router`` (x += r*a, norm, router), ``lm_moe_routes`` (expert
 GEMMs, route order) and ``lm_moe_finish_add_rmsnorm`` (combine, x += r*y,
-next layer's norm). Dense projections stay on the vendor BLAS for now; every
-other step is a hand-written kernel. There is no CPU path.
+next layer's norm). In lean decode (rows <= 128) the dense projections are
+split-K MFMA kernels (``lm_linear_splitk``) whose fp32 partials are summed
+by their consumers: ``lm_flash_decode_qkv`` (QKV reduction, RoPE, KV store
+and attention in one launch) and ``lm_add_rmsnorm_router_splitk``; a decode
+layer is then seven hand-written launches. Prefill projections use the
+vendor BLAS (F.linear). There is no CPU path.
 """
 import torch
 import torch.nn.functional as F
@@ -28,10 +32,12 @@ from . import _lib
 from .config import validate_config
 from .flash_decode import FlashDecode
 from .experts import finish_add_rmsnorm
+from .linear import linear_splitk, pick_splits
 from .norm import add_rmsnorm
 from .packed import PackedPrefill, varlen_attention
 from .rope import rope_kv_write
 from .router import add_rmsnorm_route as route_add_rmsnorm
+from .router import add_rmsnorm_route_splitk as route_add_rmsnorm_splitk
 from .router import route
 
 
@@ -93,6 +99,31 @@ class Granite:
                       cfg.attention_multiplier, self.used)
         return F.linear(a.reshape(rows, hq * d), w["self_attn.o_proj"])
 
+    def decode_splits(self, rows):
+        """K-slice counts (qkv, o_proj) of the split-K decode projections, or
+        None when a shape has no kernel (the layer then uses F.linear)."""
+        cfg = self.cfg
+        d = cfg.hidden_size // cfg.num_attention_heads
+        if d != 64 or cfg.hidden_size % 512 or cfg.hidden_size > 4096:
+            return None
+        nqkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * d
+        sq = pick_splits(rows, nqkv, cfg.hidden_size)
+        so = pick_splits(rows, cfg.hidden_size, cfg.num_attention_heads * d)
+        return (sq, so) if sq and so else None
+
+    def attention_splitk(self, z, w, cache, layer, rope_positions, active, splits):
+        """Decode layer attention on the split-K projections: the packed QKV
+        partials go to lm_flash_decode_qkv (reduction, RoPE, KV store and
+        attention in one launch), and the o_proj partials are returned for
+        the router's residual add (litemoe/model.py:47-73)."""
+        cfg = self.cfg
+        rows = z.shape[0]
+        part = linear_splitk(z, w["self_attn.qkv_proj"], splits[0])
+        flash = self._decode_attention(rows, cache)
+        a = flash.fused_qkv(part, self.cos_sin, rope_positions, active, cache.k[layer], cache.v[layer],
+                            cfg.attention_multiplier, self.used, cfg.num_attention_heads)
+        return linear_splitk(a.view(rows, -1), w["self_attn.o_proj"], splits[1])
+
     def _fused_moe(self):
         """The fused layer tail (add+norm+router, route GEMMs, combine+add+norm)
         applies when the experts run on this library with identity placement
@@ -128,10 +159,16 @@ class Granite:
         z = add_rmsnorm(x, None, r, layers[0]["input_layernorm"], eps)
         if not masked and self._fused_moe():
             k = cfg.num_experts_per_tok
+            splits = None if packed else self.decode_splits(b * s)
             for layer, w in enumerate(layers):
-                a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
-                weights, ids, z = route_add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps,
-                                                    w["block_sparse_moe.router.layer"], k, z)
+                if splits:
+                    o_part = self.attention_splitk(z, w, cache, layer, rope_positions, valid_rows, splits)
+                    weights, ids, z = route_add_rmsnorm_splitk(x, o_part, r, w["post_attention_layernorm"],
+                                                               eps, w["block_sparse_moe.router.layer"], k, z)
+                else:
+                    a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
+                    weights, ids, z = route_add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps,
+                                                        w["block_sparse_moe.router.layer"], k, z)
                 y = self.ep.backend.routes(z, w["input_linear"], w["output_linear"], ids)
                 nxt = layers[layer + 1]["input_layernorm"] if layer + 1 < len(layers) else self.w["norm"]
                 finish_add_rmsnorm(y, ids, weights, x, r, nxt, eps, z)

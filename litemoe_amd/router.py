@@ -71,3 +71,24 @@ def add_rmsnorm_route(x, a, alpha, norm_weight, eps, gate_weight, topk, z=None, 
               int(bool(renormalize)), _lib.ptr(logits_out), weights.data_ptr(), ids.data_ptr(),
               _lib.stream(x.device))
     return weights, ids, z
+
+
+def add_rmsnorm_route_splitk(x, partials, alpha, norm_weight, eps, gate_weight, topk, z=None,
+                             renormalize=True, logits_out=None):
+    """:func:`add_rmsnorm_route` with the residual branch given as split-K
+    partials ``[S, M, H]`` of the attention output projection
+    (``a = bf16(sum of slices)``, litemoe/model.py:73 then :108-113)."""
+    _lib.require_cuda(x, partials, norm_weight, gate_weight, what="router inputs")
+    if x.dtype != torch.bfloat16 or not x.is_contiguous() or gate_weight.shape[1] != x.shape[-1]:
+        raise ValueError('Router needs a contiguous BF16 [M, H] residual and [E, H] weight')
+    m, hidden = x.numel() // x.shape[-1], x.shape[-1]
+    if partials.dtype != torch.float32 or not partials.is_contiguous() or partials.shape[1:] != (m, hidden):
+        raise ValueError('Residual partials must be contiguous fp32 [S, M, H]')
+    experts = gate_weight.shape[0]
+    z = torch.empty_like(x) if z is None else z
+    weights, ids = _outputs(m, topk, x.device)
+    _lib.call("lm_add_rmsnorm_router_splitk", x.data_ptr(), partials.data_ptr(), partials.shape[0],
+              float(alpha), norm_weight.data_ptr(), float(eps), z.data_ptr(), gate_weight.data_ptr(), m,
+              hidden, experts, topk, int(bool(renormalize)), _lib.ptr(logits_out), weights.data_ptr(),
+              ids.data_ptr(), _lib.stream(x.device))
+    return weights, ids, z

@@ -1,0 +1,155 @@
+"""Split-K decode projections and their fused consumers.
+
+Bars: the projection against an fp32 product of the same bf16 operands
+(within fp32 accumulation-order error; the bf16 output within one ulp); the
+fused consumers bitwise against the unfused kernels they replace
+(reduce -> rope_kv_write -> flash_decode, reduce -> add_rmsnorm_route).
+"""
+import pytest
+import torch
+
+from litemoe_amd import _lib, flash_decode, linear, rope, router
+from litemoe_amd.cache import KVCache
+from litemoe_amd.config import ModelConfig
+from litemoe_amd.synth import normal_bf16
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def bf(shape, std=1.0, seed=0):
+    return normal_bf16(shape, std, seed)
+
+
+def ordered(t):
+    i = t.contiguous().view(torch.int16).to(torch.int32)
+    return torch.where(i >= 0, i, -(i & 0x7FFF))
+
+
+def within_ulp_or_abs(a, b, ulps, floor):
+    """Every element within ``ulps`` bf16 ulps or ``floor`` absolutely (sums
+    that cancel to near zero lose relative accuracy)."""
+    close = (ordered(a) - ordered(b)).abs() <= ulps
+    return bool((close | ((a.float() - b.float()).abs() <= floor)).all())
+
+
+@pytest.mark.parametrize("rows", [1, 7, 16, 33, 64, 128])
+@pytest.mark.parametrize("n,k", [(2560, 1536), (1536, 1536), (2048, 1024), (64, 512)])
+@torch.inference_mode()
+def test_linear_splitk_matches_fp32_product(rows, n, k):
+    a = bf((rows, k), 1.0, rows + n)
+    w = bf((n, k), 0.02, k + 1)
+    exp = a.float() @ w.float().T
+    for splits in sorted({s for s in (1, 2, 3, 4, 6, 8) if (k // 128) % s == 0 and (k // 128) // s in (1, 2, 3, 4, 6, 8)}):
+        part = linear.linear_splitk(a.to(DEV), w.to(DEV), splits)
+        assert part.shape == (splits, rows, n)
+        got = part.sum(0).cpu()
+        torch.testing.assert_close(got, exp, atol=2e-5 * k ** 0.5, rtol=1e-5)
+        out = linear.reduce(part).cpu()
+        assert within_ulp_or_abs(out, exp.to(torch.bfloat16), 1, 1e-3)
+
+
+@torch.inference_mode()
+def test_linear_splitk_strided_rows_and_unsupported_shapes():
+    a = bf((16, 2048), 1.0, 3).to(DEV)
+    w = bf((512, 1024), 0.02, 4).to(DEV)
+    view = a[:, 512:1536]  # row stride 2048
+    got = linear.linear(view, w).cpu()
+    exp = (view.float().cpu() @ w.float().cpu().T).to(torch.bfloat16)
+    assert within_ulp_or_abs(got, exp, 1, 1e-3)
+    assert linear.pick_splits(129, 512, 1024) is None
+    assert linear.pick_splits(64, 500, 1024) is None
+    with pytest.raises(_lib.NativeError):
+        linear.linear_splitk(bf((129, 1024)).to(DEV), w, 2)
+    with pytest.raises(_lib.NativeError):
+        linear.linear_splitk(bf((16, 1024)).to(DEV), w, 5)  # 8 k steps do not split in 5
+
+
+def _qkv_case(b, hq, hkv, cap, splits, seed):
+    g = torch.Generator().manual_seed(seed)
+    ncols = (hq + 2 * hkv) * 64
+    part = (torch.randn(splits, b, ncols, generator=g) * 0.7).to(DEV)
+    cos_sin, _, _ = ops.rope_tables(1e4, 64, cap, torch.bfloat16)
+    pos = torch.randint(0, cap, (b,), generator=g)
+    pos[0] = 0
+    pos[-1] = cap - 1
+    return part, cos_sin.to(DEV), pos.to(DEV)
+
+
+@pytest.mark.parametrize("b,hq,hkv,cap,attn_splits,qkv_splits", [
+    (64, 24, 8, 1280, 1, 3), (5, 24, 8, 1024, 4, 3), (3, 16, 8, 300, 3, 2), (7, 8, 8, 64, 1, 8),
+    (2, 32, 4, 2048, 16, 1)])
+@torch.inference_mode()
+def test_flash_decode_qkv_equals_unfused(b, hq, hkv, cap, attn_splits, qkv_splits):
+    part, cos_sin, pos = _qkv_case(b, hq, hkv, cap, qkv_splits, b * cap)
+    active = torch.ones(b, dtype=torch.bool, device=DEV)
+    if b > 2:
+        active[1] = False
+    used = torch.where(active, pos + 1, 1).to(torch.int32)
+    cfg = ModelConfig(num_key_value_heads=hkv, hidden_size=hq * 64, num_attention_heads=hq, num_hidden_layers=1)
+    caches = [KVCache(cfg, b, cap, DEV, torch.bfloat16) for _ in range(2)]
+    caches[0].k.normal_()
+    caches[0].v.normal_()
+    caches[1].k.copy_(caches[0].k)
+    caches[1].v.copy_(caches[0].v)
+    fd = flash_decode.FlashDecode(b, hkv, hq // hkv, cap, DEV, num_splits=attn_splits)
+    # unfused: reduce -> rope + kv store -> attention over the cache
+    qkv = linear.reduce(part)
+    q = qkv[:, :hq * 64].view(b, hq, 64)
+    k = qkv[:, hq * 64:(hq + hkv) * 64].view(b, hkv, 64)
+    v = qkv[:, (hq + hkv) * 64:].view(b, hkv, 64)
+    rope.rope_kv_write(q, k, v, pos, active, cos_sin, caches[0], 0)
+    exp = fd(q.unsqueeze(2), caches[0].k[0], caches[0].v[0], None, None, 0.125, used=used)
+    got = fd.fused_qkv(part, cos_sin, pos, active, caches[1].k[0], caches[1].v[0], 0.125, used, hq)
+    assert torch.equal(got, exp)
+    assert torch.equal(caches[1].k, caches[0].k) and torch.equal(caches[1].v, caches[0].v)
+    # and against the oracle's attention over the updated cache
+    rows = list(range(min(b, 8)))
+    ref = ops.decode_attention(q.cpu()[rows], caches[0].k[0].cpu()[rows], caches[0].v[0].cpu()[rows],
+                               used.cpu()[rows], 0.125)
+    torch.testing.assert_close(got[rows, :, 0].cpu(), ref, atol=.004, rtol=.03)
+
+
+@torch.inference_mode()
+def test_flash_decode_qkv_in_a_graph_replays_like_eager():
+    b, hq, hkv, cap = 16, 24, 8, 512
+    part, cos_sin, pos = _qkv_case(b, hq, hkv, cap, 3, 5)
+    used = (pos + 1).to(torch.int32)
+    cfg = ModelConfig(num_key_value_heads=hkv, hidden_size=hq * 64, num_attention_heads=hq, num_hidden_layers=1)
+    cache = KVCache(cfg, b, cap, DEV, torch.bfloat16)
+    cache.k.normal_()
+    cache.v.normal_()
+    fd = flash_decode.FlashDecode(b, hkv, hq // hkv, cap, DEV, num_splits=2)
+    eager = fd.fused_qkv(part, cos_sin, pos, None, cache.k[0], cache.v[0], 0.125, used, hq).clone()
+    k_after = cache.k.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            out = fd.fused_qkv(part, cos_sin, pos, None, cache.k[0], cache.v[0], 0.125, used, hq)
+    torch.cuda.current_stream().wait_stream(stream)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager) and torch.equal(cache.k, k_after)
+
+
+@pytest.mark.parametrize("splits", [1, 3, 4, 8])
+@torch.inference_mode()
+def test_add_rmsnorm_route_splitk_equals_unfused(splits):
+    m, h, e, k = 64, 1536, 40, 8
+    g = torch.Generator().manual_seed(40 + splits)
+    part = (torch.randn(splits, m, h, generator=g) * 0.5).to(DEV)
+    x = torch.randn(m, h, generator=g).to(torch.bfloat16).to(DEV)
+    w = (1 + 0.2 * torch.randn(h, generator=g)).to(torch.bfloat16).to(DEV)
+    wr = (0.02 * torch.randn(e, h, generator=g)).to(torch.bfloat16).to(DEV)
+    x1, x2 = x.clone(), x.clone()
+    l1 = torch.empty(m, e, device=DEV, dtype=torch.bfloat16)
+    l2 = torch.empty(m, e, device=DEV, dtype=torch.bfloat16)
+    w1, i1, z1 = router.add_rmsnorm_route_splitk(x1, part, 0.22, w, 1e-6, wr, k, logits_out=l1)
+    a = linear.reduce(part)
+    w2, i2, z2 = router.add_rmsnorm_route(x2, a, 0.22, w, 1e-6, wr, k, logits_out=l2)
+    assert torch.equal(x1, x2) and torch.equal(z1, z2) and torch.equal(l1, l2)
+    assert torch.equal(i1, i2) and torch.equal(w1, w2)
