@@ -35,8 +35,29 @@ struct Partial {
   float *l;  // [batch, q_heads, splits]
 };
 
+// Scores and running maxima are kept in log2 units (scale * log2(e) folded
+// into the q.k product), so every exponential is a bare v_exp_f32.
 __device__ __forceinline__ float merge_factor(float m, float mnew) {
-  return m == -INFINITY ? 0.f : __expf(m - mnew);
+  return m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Dot product of the 8 bf16 channels of two 16-byte words, four
+// v_dot2_f32_bf16 in channel-pair order. The pairs are taken with
+// shufflevector from a bf16x8 view (bit-casting indexed u32 lanes in an
+// unrolled loop compiled to four dots of lane 0).
+__device__ __forceinline__ float dot8_bf16(const u32x4 &a, const u32x4 &b) {
+  const bf16x8 av = as_bf16x8(a), bv = as_bf16x8(b);
+  float d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 0, 1),
+                                            __builtin_shufflevector(bv, bv, 0, 1), 0.f, false);
+  d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 2, 3),
+                                      __builtin_shufflevector(bv, bv, 2, 3), d, false);
+  d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 4, 5),
+                                      __builtin_shufflevector(bv, bv, 4, 5), d, false);
+  d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 6, 7),
+                                      __builtin_shufflevector(bv, bv, 6, 7), d, false);
+  return d;
 }
 
 // The projection-fused form (lm_flash_decode_qkv): q, k and v of the row
@@ -73,7 +94,7 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
   __shared__ float sm_m[kWaves][G];
   __shared__ float sm_l[kWaves][G];
   __shared__ float sm_qkv[kFused ? G + 2 : 1][kD];
-  __shared__ float sm_knew[kFused ? kD : 1];
+  __shared__ u32x4 sm_knew[kFused ? kLanesPerKey : 1];  // rotated new key, bf16 words per lane group
   const int split = blockIdx.x, h = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -120,10 +141,13 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
   const int first = k0 + wave * kKeysPerWave + ks;  // key of group 0 in iteration 0
   const int niter = k1 > k0 ? (k1 - k0 + kKeysPerIter - 1) / kKeysPerIter : 0;
 
+  // Every KV load is unconditional, its key clamped into [0, k1): a load
+  // under a branch would make the compiler's wait counts fall back to
+  // waiting for all loads, draining the prefetch.
   auto load = [&](u32x4 *kb, u32x4 *vb, int it) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const int j = min(first + it * kKeysPerIter + u * kSlots, k1 - 1);
+      const int j = max(min(first + it * kKeysPerIter + u * kSlots, k1 - 1), 0);
       kb[u] = *reinterpret_cast<const u32x4 *>(kbase + (int64_t)j * kD);
       vb[u] = *reinterpret_cast<const u32x4 *>(vbase + (int64_t)j * kD);
     }
@@ -139,10 +163,12 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
     cs_s = *reinterpret_cast<const u32x4 *>(cs + kD / 2 + c0);
   }
   u32x4 ka[kU], va[kU], kb2[kU], vb2[kU];
-  if (niter > 0) load(ka, va, 0);
-  if (niter > 1) load(kb2, vb2, 1);
+  load(ka, va, 0);
+  load(kb2, vb2, 1);
 
-  float qv[G][8];
+  // q stays bf16 (packed pairs); the softmax scale is applied to the dot.
+  u32x4 qw[G];
+  const float sl2 = scale * 1.4426950408889634f;
   if constexpr (kFused) {
     float cf[8], sf[8];
     unpack8(cs_c, cf);
@@ -175,9 +201,10 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
     };
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      rotated(g, qv[g]);
+      float qf[8];
+      rotated(g, qf);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qv[g][i] *= scale;
+      for (int i = 0; i < 4; ++i) qw[g][i] = pack_bf16(qf[2 * i], qf[2 * i + 1]);
     }
     // The rotated new key goes to LDS (for the substitution) and, with the
     // value, to the cache.
@@ -187,24 +214,19 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
       const int64_t at = (((int64_t)b * kv_heads + h) * capacity + pnew) * kD + dc * 8;
       u32x4 ko, vo;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sm_knew[dc * 8 + i] = knew[i];
-#pragma unroll
       for (int i = 0; i < 4; ++i) {
         ko[i] = pack_bf16(knew[2 * i], knew[2 * i + 1]);
         vo[i] = pack_bf16(sm_qkv[G + 1][dc * 8 + 2 * i], sm_qkv[G + 1][dc * 8 + 2 * i + 1]);
       }
+      sm_knew[dc] = ko;
       *reinterpret_cast<u32x4 *>(kc + at) = ko;
       *reinterpret_cast<u32x4 *>(vc + at) = vo;
     }
     if (own) __syncthreads();  // uniform across the workgroup
   } else {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const bf16 *qp = q + b * qs0 + (int64_t)(h * G + g) * qs1 + dc * 8;
-      unpack8(*reinterpret_cast<const u32x4 *>(qp), qv[g]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qv[g][i] *= scale;
-    }
+    for (int g = 0; g < G; ++g)
+      qw[g] = *reinterpret_cast<const u32x4 *>(q + b * qs0 + (int64_t)(h * G + g) * qs1 + dc * 8);
   }
   float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -221,21 +243,14 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
     for (int u = 0; u < kU; ++u) {
       const int j = first + it * kKeysPerIter + u * kSlots;
       const bool ok = j < k1;
-      float kf[8];
-      unpack8(kb[u], kf);
+      u32x4 kw = kb[u];
       if constexpr (kFused) {
-        if (own && j == pnew) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) kf[i] = sm_knew[dc * 8 + i];
-        }
+        if (own && j == pnew) kw = sm_knew[dc];
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], kf[i], d);
-        d = dpp_sum8(d);
-        s[u][g] = ok ? d : -INFINITY;
+        const float d = dpp_sum8(dot8_bf16(qw[g], kw));
+        s[u][g] = ok ? d * sl2 : -INFINITY;
       }
     }
     float vf[kU][8];
@@ -255,14 +270,17 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
 #pragma unroll
       for (int u = 0; u < kU; ++u) mx = fmaxf(mx, s[u][g]);
       if (mx == -INFINITY) continue;
-      const float corr = merge_factor(m[g], mx);
-      m[g] = mx;
-      l[g] *= corr;
+      // Rescale only when the running max moves (the factor would be 1).
+      if (mx > m[g]) {
+        const float corr = merge_factor(m[g], mx);
+        m[g] = mx;
+        l[g] *= corr;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] *= corr;
+        for (int i = 0; i < 8; ++i) acc[g][i] *= corr;
+      }
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
-        const float p = s[u][g] == -INFINITY ? 0.f : __expf(s[u][g] - mx);
+        const float p = s[u][g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[u][g] - mx);
         l[g] += p;
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[u][i], acc[g][i]);
@@ -270,14 +288,13 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
     }
   };
 
-  // Two iterations in flight: iteration it+2 is issued once it is consumed.
+  // Two iterations in flight: iteration it+2 is issued once it is consumed
+  // (past the end the loads repeat the last key and are not used).
   for (int it = 0; it < niter; it += 2) {
     compute(ka, va, it);
-    if (it + 2 < niter) load(ka, va, it + 2);
-    if (it + 1 < niter) {
-      compute(kb2, vb2, it + 1);
-      if (it + 3 < niter) load(kb2, vb2, it + 3);
-    }
+    load(ka, va, it + 2);
+    if (it + 1 < niter) compute(kb2, vb2, it + 1);
+    load(kb2, vb2, it + 3);
   }
 
   // Merge the 8 key slots of the wave (lanes with equal dc).
