@@ -319,7 +319,7 @@ int lm_add_rmsnorm_router(void *x, const void *a, float alpha,
  *   lm_add_rmsnorm_router. Bitwise equal to lm_linear_splitk_reduce followed
  * by lm_add_rmsnorm_router. Fuses the o_proj output of litemoe/model.py:73
  * into :108-113. a_partials: fp32 [a_splits][tokens][hidden], 1 <= a_splits
- * <= 8; hidden a multiple of 512 up to 4096 (else LM_EUNSUPPORTED). */
+ * <= 4; hidden a multiple of 512 up to 2048 (else LM_EUNSUPPORTED). */
 int lm_add_rmsnorm_router_splitk(void *x, const float *a_partials,
                                  int64_t a_splits, float alpha,
                                  const void *norm_weight, float eps, void *z,

@@ -101,6 +101,59 @@ __device__ void select_topk(const float *logit, int experts, int topk, int renor
   }
 }
 
+// select_topk for experts <= 64, run by wave 0 alone with no LDS round trip
+// or barrier: logits are bf16, so (orderable bf16 bits, ~id) fits a 32-bit
+// key; lane e holds expert e's key and counts the larger keys broadcast with
+// readlane; the lane of each rank is found with a ballot. The selection, the
+// weights and the order of the softmax denominator's sum are those of
+// select_topk. The caller synchronises before (logits in LDS).
+__device__ void select_topk_wave(const float *logit, int experts, int topk, int renormalize,
+                                 float *__restrict__ tw, int32_t *__restrict__ tid) {
+  const int t = threadIdx.x;
+  if (t >= kWave) return;
+  uint32_t key = 0u;  // below every real key
+  float v = 0.f;
+  if (t < experts) {
+    v = logit[t];
+    uint32_t h = __float_as_uint(v) >> 16;  // exact: logits are bf16 values
+    if ((h & 0x7fffu) > 0x7f80u) h = 0x7fc0u;
+    const uint32_t ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+    key = (ord << 16) | (0xffffu - (uint32_t)t);
+  }
+  int rank = 0;
+  for (int e = 0; e < experts; ++e)
+    rank += (uint32_t)__builtin_amdgcn_readlane((int)key, e) > key;
+  if (t >= experts) rank = kWave;
+  const int top = __builtin_ctzll(__ballot(rank == 0));
+  const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
+  const float ex = expf(v - m);
+  float denom = 0.f;
+  if (renormalize) {
+    for (int r = 0; r < topk; ++r) {
+      const int at = __builtin_ctzll(__ballot(rank == r));
+      denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), at));
+    }
+  } else {
+    for (int e = 0; e < experts; ++e)
+      denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), e));
+  }
+  if (rank < topk) {
+    tw[rank] = ex / denom;
+    tid[rank] = t;
+  }
+}
+
+// Both selections end with the outputs written; neither needs a barrier
+// after it.
+__device__ __forceinline__ void select(const float *logit, int experts, int topk, int renormalize,
+                                       float *sel_val, int *sel_id, float *__restrict__ tw,
+                                       int32_t *__restrict__ tid) {
+  if (experts <= kWave)
+    select_topk_wave(logit, experts, topk, renormalize, tw, tid);
+  else
+    select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw, tid);
+}
+
 // One workgroup per token: stage the row in LDS, GEMV, select.
 __global__ void __launch_bounds__(kRouterThreads)
 router_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ wr, int hidden, int experts,
@@ -117,7 +170,7 @@ router_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ wr, int hidde
   __syncthreads();
   router_gemv(zs, wr, nvec, experts, logit, logits_out ? logits_out + row * experts : nullptr);
   __syncthreads();
-  select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
+  select(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
 }
 
 __global__ void __launch_bounds__(kRouterThreads)
@@ -130,7 +183,7 @@ topk_from_logits_kernel(const bf16 *__restrict__ logits, int experts, int topk, 
   for (int e = threadIdx.x; e < experts; e += kRouterThreads)
     logit[e] = bf16_to_f32(logits[row * experts + e]);
   __syncthreads();
-  select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
+  select(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
 }
 
 // Residual add + RMSNorm + router GEMV + top-k, one workgroup per token.
@@ -194,7 +247,7 @@ add_norm_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float a
   __syncthreads();
   router_gemv(zs, wr, nvec, experts, logit, logits_out ? logits_out + row * experts : nullptr);
   __syncthreads();
-  select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
+  select(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
 }
 
 // Latency-bound variant for hidden = 512 * NV: 1024 threads, and every load
@@ -254,7 +307,7 @@ __device__ __forceinline__ void gate_round(const u32x4 *zs, int experts, int rou
   }
 }
 
-constexpr int kMaxResidualSplits = 8;
+constexpr int kMaxResidualSplits = 4;  // partial slices held in VGPRs (128 per lane at 1024 threads)
 
 // kNorm: z = rmsnorm(x [+ alpha*a]) is routed (and x, z are written);
 // otherwise x itself is routed. kPart: a is given as fp32 split-K partials
@@ -287,13 +340,15 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
       const int i = min(t + v * kRouterThreads, nvec - 1);
       xv[v] = xr[i];
       if constexpr (kPart) {
+        // Unconditional loads (slice index clamped): a load under a branch
+        // would make the compiler wait for every load before the first use.
         const f32x4 *src = reinterpret_cast<const f32x4 *>(ap + row * nvec * 8) + 2 * i;
 #pragma unroll
-        for (int s = 0; s < kMaxResidualSplits; ++s)
-          if (s < asplits) {
-            pv[v][s][0] = src[(int64_t)s * gridDim.x * nvec * 2];
-            pv[v][s][1] = src[(int64_t)s * gridDim.x * nvec * 2 + 1];
-          }
+        for (int s = 0; s < kMaxResidualSplits; ++s) {
+          const int64_t at = (int64_t)min(s, asplits - 1) * gridDim.x * nvec * 2;
+          pv[v][s][0] = src[at];
+          pv[v][s][1] = src[at + 1];
+        }
       } else if constexpr (kAdd) {
         av[v] = ar[i];
       }
@@ -315,11 +370,11 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
         if constexpr (kPart) {
           f32x4 lo = pv[v][0][0], hi = pv[v][0][1];
 #pragma unroll
-          for (int s = 1; s < kMaxResidualSplits; ++s)
-            if (s < asplits) {
-              lo += pv[v][s][0];
-              hi += pv[v][s][1];
-            }
+          for (int s = 1; s < kMaxResidualSplits; ++s) {
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+            lo += s < asplits ? pv[v][s][0] : zero;  // + 0 leaves the sum unchanged
+            hi += s < asplits ? pv[v][s][1] : zero;
+          }
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             g[c] = round_bf16(lo[c]);
@@ -379,7 +434,7 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
     gate_round<NV>(zs, experts, round, w, logit, lrow);
   }
   __syncthreads();
-  select_topk(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
+  select(logit, experts, topk, renormalize, sel_val, sel_id, tw + row * topk, tid + row * topk);
 }
 
 // hidden = 512 * NV for an instantiated NV, else 0.
@@ -402,9 +457,21 @@ void launch_fast_router(int nv, int64_t tokens, bf16 *x, const bf16 *a, float al
         x, a, alpha, nw, eps, z, wr, experts, topk, renormalize, logits_out, tw, tid, ap,      \
         asplits);                                                                              \
     break;
-    LM_FAST_ROUTER(1) LM_FAST_ROUTER(2) LM_FAST_ROUTER(3) LM_FAST_ROUTER(4) LM_FAST_ROUTER(6)
-    LM_FAST_ROUTER(8)
+    LM_FAST_ROUTER(1) LM_FAST_ROUTER(2) LM_FAST_ROUTER(3) LM_FAST_ROUTER(4)
 #undef LM_FAST_ROUTER
+    // hidden 3072/4096 with fp32 partials would not fit 128 VGPRs per lane
+    case 6:
+      if constexpr (!kPart)
+        fast_router_kernel<6, kNorm, kAdd, false><<<grid, kFastThreads, 0, s>>>(
+            x, a, alpha, nw, eps, z, wr, experts, topk, renormalize, logits_out, tw, tid, ap,
+            asplits);
+      break;
+    case 8:
+      if constexpr (!kPart)
+        fast_router_kernel<8, kNorm, kAdd, false><<<grid, kFastThreads, 0, s>>>(
+            x, a, alpha, nw, eps, z, wr, experts, topk, renormalize, logits_out, tw, tid, ap,
+            asplits);
+      break;
   }
 }
 
@@ -576,7 +643,7 @@ extern "C" int lm_add_rmsnorm_router_splitk(void *x, const float *a_partials, in
                                             void *stream) {
   LM_REQUIRE(tokens >= 0 && hidden > 0 && experts > 0 && topk > 0 && a_splits > 0);
   const int nv = fast_nv(hidden);
-  if (!nv || experts > kMaxExperts || topk > kMaxTopk || topk > experts ||
+  if (!nv || nv > 4 || experts > kMaxExperts || topk > kMaxTopk || topk > experts ||
       a_splits > kMaxResidualSplits)
     return LM_EUNSUPPORTED;
   if (tokens == 0) return LM_OK;

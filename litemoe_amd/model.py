@@ -104,11 +104,12 @@ class Granite:
         None when a shape has no kernel (the layer then uses F.linear)."""
         cfg = self.cfg
         d = cfg.hidden_size // cfg.num_attention_heads
-        if d != 64 or cfg.hidden_size % 512 or cfg.hidden_size > 4096:
+        # lm_add_rmsnorm_router_splitk: hidden 512*{1..4}, at most 4 slices
+        if d != 64 or cfg.hidden_size % 512 or cfg.hidden_size > 2048:
             return None
         nqkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * d
         sq = pick_splits(rows, nqkv, cfg.hidden_size)
-        so = pick_splits(rows, cfg.hidden_size, cfg.num_attention_heads * d)
+        so = pick_splits(rows, cfg.hidden_size, cfg.num_attention_heads * d, max_splits=4)
         return (sq, so) if sq and so else None
 
     def attention_splitk(self, z, w, cache, layer, rope_positions, active, splits):

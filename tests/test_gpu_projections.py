@@ -136,7 +136,7 @@ def test_flash_decode_qkv_in_a_graph_replays_like_eager():
         assert torch.equal(out, eager) and torch.equal(cache.k, k_after)
 
 
-@pytest.mark.parametrize("splits", [1, 3, 4, 8])
+@pytest.mark.parametrize("splits", [1, 2, 3, 4])
 @torch.inference_mode()
 def test_add_rmsnorm_route_splitk_equals_unfused(splits):
     m, h, e, k = 64, 1536, 40, 8
@@ -153,3 +153,17 @@ def test_add_rmsnorm_route_splitk_equals_unfused(splits):
     w2, i2, z2 = router.add_rmsnorm_route(x2, a, 0.22, w, 1e-6, wr, k, logits_out=l2)
     assert torch.equal(x1, x2) and torch.equal(z1, z2) and torch.equal(l1, l2)
     assert torch.equal(i1, i2) and torch.equal(w1, w2)
+
+
+@torch.inference_mode()
+def test_add_rmsnorm_route_splitk_limits():
+    x = torch.zeros(4, 1536, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(1536, dtype=torch.bfloat16, device=DEV)
+    wr = torch.zeros(40, 1536, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.NativeError):  # more than 4 slices
+        router.add_rmsnorm_route_splitk(x, torch.zeros(5, 4, 1536, device=DEV), 0.2, w, 1e-6, wr, 8)
+    x3 = torch.zeros(4, 3072, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.NativeError):  # hidden above 2048
+        router.add_rmsnorm_route_splitk(x3, torch.zeros(2, 4, 3072, device=DEV), 0.2,
+                                        torch.ones(3072, dtype=torch.bfloat16, device=DEV), 1e-6,
+                                        torch.zeros(40, 3072, dtype=torch.bfloat16, device=DEV), 8)
