@@ -26,6 +26,7 @@ constexpr int kThreads = kWaves * kWave;
 constexpr int kLanesPerKey = 8;
 constexpr int kSlots = kWave / kLanesPerKey;  // key slots per wave
 constexpr int kU = 2;                         // key groups per lane per iteration
+static_assert(kU == 2, "P.V pairs the two keys of a lane's iteration");
 constexpr int kKeysPerWave = kSlots * kU;     // 16
 constexpr int kKeysPerIter = kKeysPerWave * kWaves;
 
@@ -37,6 +38,10 @@ struct Partial {
 
 // Scores and running maxima are kept in log2 units (scale * log2(e) folded
 // into the q.k product), so every exponential is a bare v_exp_f32.
+// Running max of a state that has seen no key: finite, so exp2(kEmpty - m)
+// and exp2(-inf - kEmpty) are exactly 0 and the loop needs no special case.
+constexpr float kEmpty = -1e30f;
+
 __device__ __forceinline__ float merge_factor(float m, float mnew) {
   return m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
 }
@@ -231,7 +236,7 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
   float m[G], l[G], acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
+    m[g] = kEmpty;
     l[g] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
@@ -253,23 +258,32 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
         s[u][g] = ok ? d * sl2 : -INFINITY;
       }
     }
-    float vf[kU][8];
+    u32x4 vw[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      unpack8(vb[u], vf[u]);
+      vw[u] = vb[u];
       if constexpr (kFused) {
         if (own && first + it * kKeysPerIter + u * kSlots == pnew) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) vf[u][i] = sm_qkv[G + 1][dc * 8 + i];
+          for (int i = 0; i < 4; ++i)
+            vw[u][i] = pack_bf16(sm_qkv[G + 1][dc * 8 + 2 * i], sm_qkv[G + 1][dc * 8 + 2 * i + 1]);
         }
       }
+    }
+    // Channel c's values of the two keys as one bf16 pair (v_perm_b32), so
+    // P.V is one v_dot2_f32_bf16 per channel with P rounded to bf16 (as a
+    // flash-attention P.V on matrix cores rounds it).
+    uint32_t vp[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      vp[2 * i] = __builtin_amdgcn_perm(vw[1][i], vw[0][i], 0x05040100u);
+      vp[2 * i + 1] = __builtin_amdgcn_perm(vw[1][i], vw[0][i], 0x07060302u);
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float mx = m[g];
 #pragma unroll
       for (int u = 0; u < kU; ++u) mx = fmaxf(mx, s[u][g]);
-      if (mx == -INFINITY) continue;
       // Rescale only when the running max moves (the factor would be 1).
       if (mx > m[g]) {
         const float corr = merge_factor(m[g], mx);
@@ -278,13 +292,18 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[g][i] *= corr;
       }
+      // masked keys: exp2(-inf) = 0
+      const float p0 = __builtin_amdgcn_exp2f(s[0][g] - mx);
+      const float p1 = __builtin_amdgcn_exp2f(s[1][g] - mx);
+      l[g] += p0;
+      l[g] += p1;
+      bf16x2 pp;
+      pp[0] = (__bf16)p0;
+      pp[1] = (__bf16)p1;
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const float p = s[u][g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[u][g] - mx);
-        l[g] += p;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[u][i], acc[g][i]);
-      }
+      for (int c = 0; c < 8; ++c)
+        acc[g][c] = __builtin_amdgcn_fdot2_f32_bf16(pp, __builtin_bit_cast(bf16x2, vp[c]),
+                                                    acc[g][c], false);
     }
   };
 
