@@ -363,6 +363,42 @@ int lm_moe_finish_add_rmsnorm(const void *y, const int32_t *ids,
                               float eps, void *z, int64_t tokens,
                               int64_t hidden, int64_t topk, void *stream);
 
+/* -------------------------------------------------- greedy decode step ends -- */
+
+/* The start of one decode step, per row b (one launch):
+ *   valid[b] = active[b];  positions[b] = valid[b] ? length[b] : 0;
+ *   used[b] = positions[b] + 1;
+ *   x[b] = bf16(embedding[next[b]] * multiplier);  z[b] = rmsnorm(x[b]).
+ * Replaces litemoe/engine.py:89-91 (valid, positions) with model.py:103
+ * (used, lean decode), :104 (embedding) and :106 (first layer's norm,
+ * lm_rmsnorm's rounding). active/valid are bool bytes; length/next int64;
+ * next is clamped to [0, vocab). hidden a multiple of 8, at most 4096
+ * (else LM_EUNSUPPORTED). */
+int lm_decode_prologue(const uint8_t *active, const int64_t *length,
+                       const int64_t *next, const void *embedding,
+                       float multiplier, const void *norm_weight, float eps,
+                       void *x, void *z, uint8_t *valid, int64_t *positions,
+                       int32_t *used, int64_t rows, int64_t hidden,
+                       int64_t vocab, void *stream);
+
+/* The end of one greedy decode step, per row b (one launch):
+ *   candidate = argmax_v bf16(logits[b][v] * (1 / logits_scaling)), the
+ *   first index of the maximum (torch.argmax; NaN counts as the maximum);
+ *   emit[b] = (candidate, generated[b], valid[b]);
+ *   length[b] += valid[b];  generated[b] += valid[b];
+ *   if valid[b]: next[b] = candidate;
+ *   done = generated[b] >= budget[b] || (!ignore_eos && candidate in eos);
+ *   active[b] = valid[b] && !done.
+ * Replaces litemoe/model.py:127 (/ logits_scaling) and engine.py:92-102.
+ * logits: bf16 [rows][ld] raw head output; emit int64 [rows][3]; eos int64
+ * [neos]. */
+int lm_greedy_epilogue(const void *logits, int64_t ld, float logits_scaling,
+                       int64_t vocab, int64_t rows, const uint8_t *valid,
+                       int64_t *next, int64_t *length, int64_t *generated,
+                       const int64_t *budget, uint8_t *active, int64_t *emit,
+                       const int64_t *eos, int64_t neos, int ignore_eos,
+                       void *stream);
+
 #ifdef __cplusplus
 }
 #endif

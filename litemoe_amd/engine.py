@@ -101,6 +101,11 @@ class Engine:
 
     def decode_step(self):
         s = self.state
+        if getattr(self.model, "decode_lean", False) and self.model.greedy_supported():
+            # Lean decode: the step's set-up and its argmax/state update run
+            # as one kernel each around the layers (same tokens and state).
+            self.model.greedy_step(s, self.emit, self.eos, self.ignore_eos, self.cache)
+            return
         valid = s["active"].clone()
         positions = torch.where(valid, s["length"], 0)[:, None]
         logits = self.model.forward(s["next"][:, None], positions, valid[:, None], self.cache)

@@ -39,6 +39,7 @@ from .rope import rope_kv_write
 from .router import add_rmsnorm_route as route_add_rmsnorm
 from .router import add_rmsnorm_route_splitk as route_add_rmsnorm_splitk
 from .router import route
+from .step import decode_prologue, greedy_epilogue
 
 
 class Granite:
@@ -132,6 +133,51 @@ class Granite:
         return getattr(self.ep.backend, "native", False) and all(
             w["logical"].numel() == 0 for w in self.w["layers"])
 
+    def _fused_layers(self, x, z, cache, rope_positions, valid_rows, flat_positions, slot):
+        """The layer stack on the fused tail: per layer attention, then
+        add+norm+router, the route GEMMs and combine+add+next norm. ``x`` is
+        the residual stream and ``z`` the normalised input of the first
+        layer; on return ``z`` holds the final norm's output."""
+        cfg = self.cfg
+        layers = self.w["layers"]
+        r, eps, k = cfg.residual_multiplier, cfg.rms_norm_eps, cfg.num_experts_per_tok
+        splits = None if isinstance(slot, PackedPrefill) else self.decode_splits(x.shape[0])
+        for layer, w in enumerate(layers):
+            if splits:
+                o_part = self.attention_splitk(z, w, cache, layer, rope_positions, valid_rows, splits)
+                weights, ids, z = route_add_rmsnorm_splitk(x, o_part, r, w["post_attention_layernorm"],
+                                                           eps, w["block_sparse_moe.router.layer"], k, z)
+            else:
+                a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
+                weights, ids, z = route_add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps,
+                                                    w["block_sparse_moe.router.layer"], k, z)
+            y = self.ep.backend.routes(z, w["input_linear"], w["output_linear"], ids)
+            nxt = layers[layer + 1]["input_layernorm"] if layer + 1 < len(layers) else self.w["norm"]
+            finish_add_rmsnorm(y, ids, weights, x, r, nxt, eps, z)
+        return z
+
+    def greedy_supported(self):
+        """Whether :meth:`greedy_step` applies: lean decode on the fused tail,
+        and a hidden size the prologue kernel takes."""
+        h = self.cfg.hidden_size
+        return bool(self.decode_lean) and self._fused_moe() and h % 8 == 0 and h <= 4096
+
+    def greedy_step(self, state, emit, eos, ignore_eos, cache):
+        """One lean greedy decode step from the engine's state to its update:
+        prologue kernel (valid, positions, ``used``, embedding, first norm),
+        the fused layers, the raw head product and the epilogue kernel
+        (argmax of ``logits / logits_scaling``, emit row, state update).
+        Same tokens and state as litemoe/engine.py:87-102 around this model's
+        forward (model.py:95-127) in lean decode."""
+        cfg = self.cfg
+        x, z, valid, positions, used = decode_prologue(
+            state["active"], state["length"], state["next"], self.w["embedding"],
+            cfg.embedding_multiplier, self.w["layers"][0]["input_layernorm"], cfg.rms_norm_eps)
+        self.used = used
+        z = self._fused_layers(x, z, cache, positions, valid, positions, None)
+        greedy_epilogue(F.linear(z, self.w["head"]), cfg.logits_scaling, valid, state, emit, eos,
+                        ignore_eos)
+
     def forward(self, tokens, positions, valid, cache, slot=None, last=None, communication_tokens=None):
         cfg = self.cfg
         packed = isinstance(slot, PackedPrefill)
@@ -159,20 +205,7 @@ class Granite:
         layers = self.w["layers"]
         z = add_rmsnorm(x, None, r, layers[0]["input_layernorm"], eps)
         if not masked and self._fused_moe():
-            k = cfg.num_experts_per_tok
-            splits = None if packed else self.decode_splits(b * s)
-            for layer, w in enumerate(layers):
-                if splits:
-                    o_part = self.attention_splitk(z, w, cache, layer, rope_positions, valid_rows, splits)
-                    weights, ids, z = route_add_rmsnorm_splitk(x, o_part, r, w["post_attention_layernorm"],
-                                                               eps, w["block_sparse_moe.router.layer"], k, z)
-                else:
-                    a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
-                    weights, ids, z = route_add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps,
-                                                        w["block_sparse_moe.router.layer"], k, z)
-                y = self.ep.backend.routes(z, w["input_linear"], w["output_linear"], ids)
-                nxt = layers[layer + 1]["input_layernorm"] if layer + 1 < len(layers) else self.w["norm"]
-                finish_add_rmsnorm(y, ids, weights, x, r, nxt, eps, z)
+            z = self._fused_layers(x, z, cache, rope_positions, valid_rows, flat_positions, slot)
         else:
             y = None
             for layer, w in enumerate(layers):

@@ -1,0 +1,77 @@
+"""The two ends of a greedy decode step, each one gfx950 launch.
+
+``decode_prologue`` replaces the step's set-up (litemoe/engine.py:89-91,
+model.py:103-106): valid rows, positions, the attention's ``used`` lengths,
+the scaled embedding and the first layer's RMSNorm. ``greedy_epilogue``
+replaces the logits scaling and everything after the forward
+(model.py:127, engine.py:92-102): the argmax, the emit row and the state
+update. Both keep the reference's arithmetic, so a step through them emits
+the same tokens and leaves the same state as the reference's torch ops.
+"""
+import torch
+
+from . import _lib
+
+
+def _bool_bytes(t):
+    if t.dtype != torch.bool or not t.is_contiguous():
+        raise ValueError("expected a contiguous bool tensor")
+    return t.view(torch.uint8)
+
+
+def decode_prologue(active, length, next_tokens, embedding, multiplier, norm_weight, eps):
+    """Returns ``(x, z, valid, positions, used)`` for one decode step.
+
+    ``valid = active``; ``positions = where(valid, length, 0)``;
+    ``used = int32(positions + 1)``; ``x = embedding[next] * multiplier``
+    (bf16); ``z = rmsnorm(x, norm_weight, eps)``.
+    """
+    _lib.require_cuda(active, length, next_tokens, embedding, norm_weight, what="decode prologue inputs")
+    rows = active.shape[0]
+    vocab, hidden = embedding.shape
+    if length.dtype != torch.int64 or next_tokens.dtype != torch.int64:
+        raise ValueError("length and next must be int64")
+    if embedding.dtype != torch.bfloat16 or norm_weight.dtype != torch.bfloat16:
+        raise ValueError("embedding and norm weight must be bf16")
+    if not (embedding.is_contiguous() and norm_weight.is_contiguous() and length.is_contiguous()
+            and next_tokens.is_contiguous()) or norm_weight.numel() != hidden:
+        raise ValueError("contiguous [vocab, hidden] embedding and [hidden] norm weight required")
+    dev = embedding.device
+    x = torch.empty(rows, hidden, dtype=torch.bfloat16, device=dev)
+    z = torch.empty_like(x)
+    valid = torch.empty(rows, dtype=torch.bool, device=dev)
+    positions = torch.empty(rows, dtype=torch.int64, device=dev)
+    used = torch.empty(rows, dtype=torch.int32, device=dev)
+    _lib.call("lm_decode_prologue", _bool_bytes(active).data_ptr(), length.data_ptr(),
+              next_tokens.data_ptr(), embedding.data_ptr(), float(multiplier), norm_weight.data_ptr(),
+              float(eps), x.data_ptr(), z.data_ptr(), valid.view(torch.uint8).data_ptr(),
+              positions.data_ptr(), used.data_ptr(), rows, hidden, vocab, _lib.stream(dev))
+    return x, z, valid, positions, used
+
+
+def greedy_epilogue(logits, logits_scaling, valid, state, emit, eos, ignore_eos):
+    """Greedy token choice and the engine's state update, in place.
+
+    ``logits`` is the raw head output ``[rows, vocab]`` (before
+    ``/ logits_scaling``); ``state`` holds the engine's ``next``,
+    ``length``, ``generated``, ``budget`` (int64) and ``active`` (bool);
+    ``emit`` is ``[rows, 3]`` int64; ``eos`` an int64 tensor of stop ids.
+    """
+    _lib.require_cuda(logits, valid, emit, eos, what="greedy epilogue inputs")
+    rows, vocab = logits.shape
+    if logits.dtype != torch.bfloat16 or logits.stride(1) != 1:
+        raise ValueError("logits must be bf16 with unit column stride")
+    for name in ("next", "length", "generated", "budget"):
+        t = state[name]
+        if t.dtype != torch.int64 or not t.is_contiguous() or t.shape != (rows,):
+            raise ValueError(f"state[{name!r}] must be contiguous int64 [rows]")
+    if emit.dtype != torch.int64 or emit.shape != (rows, 3) or not emit.is_contiguous():
+        raise ValueError("emit must be contiguous int64 [rows, 3]")
+    if eos.dtype != torch.int64 or not eos.is_contiguous():
+        raise ValueError("eos must be a contiguous int64 tensor")
+    _lib.call("lm_greedy_epilogue", logits.data_ptr(), logits.stride(0), float(logits_scaling), vocab,
+              rows, _bool_bytes(valid).data_ptr(), state["next"].data_ptr(), state["length"].data_ptr(),
+              state["generated"].data_ptr(), state["budget"].data_ptr(),
+              _bool_bytes(state["active"]).data_ptr(), emit.data_ptr(),
+              eos.data_ptr() if eos.numel() else None, eos.numel(), int(bool(ignore_eos)),
+              _lib.stream(logits.device))
