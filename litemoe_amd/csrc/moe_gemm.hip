@@ -31,6 +31,13 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxScanRows = 256;
 
+// How a workgroup finds its routes and when it loads its weight tile.
+enum RouteMode : int {
+  kBlocks = 0,        // lm_moe_align blocks; weights after the block lookup
+  kScanLazy = 1,      // scan of topk_ids; weights only once routes are found
+  kScanPrefetch = 2,  // scan of topk_ids; weights issued before the scan
+};
+
 // Block b of the per-expert blocks of block_rows routes.
 __device__ __forceinline__ bool find_block(const int32_t *__restrict__ offsets, int experts, int bm,
                                            int b, int &e_out, int &r0, int &r1) {
@@ -58,8 +65,8 @@ __device__ __forceinline__ bool find_block(const int32_t *__restrict__ offsets, 
 constexpr int kScanIters = 8;  // routes <= kWaves * kScanIters * 64 = 2048
 
 struct ScanIds {
-  int id[kScanIters];
-  int begin;
+  int id[kScanIters];  // ids[begin + it*64 + lane], valid below end
+  int begin, end;
 };
 
 __device__ __forceinline__ ScanIds load_ids(const int32_t *__restrict__ ids, int routes) {
@@ -68,11 +75,13 @@ __device__ __forceinline__ ScanIds load_ids(const int32_t *__restrict__ ids, int
   ScanIds s;
   s.begin = wave * seg;
   const int end = min(routes, s.begin + seg);
+  // Unconditional loads at clamped indices, masked in scan_ids: a load
+  // under a branch (or its mask computed here) would make the compiler wait
+  // for these loads before the weight prefetch is issued, or for every load
+  // in flight before the scan.
 #pragma unroll
-  for (int it = 0; it < kScanIters; ++it) {
-    const int r = s.begin + it * kWave + lane;
-    s.id[it] = r < end ? ids[r] : -1;
-  }
+  for (int it = 0; it < kScanIters; ++it) s.id[it] = ids[min(s.begin + it * kWave + lane, routes - 1)];
+  s.end = end;
   return s;
 }
 
@@ -83,7 +92,8 @@ __device__ int scan_ids(const ScanIds &s, int e, int *list, int *wave_count) {
   const uint64_t below = (1ull << lane) - 1ull;
   int count = 0;
 #pragma unroll
-  for (int it = 0; it < kScanIters; ++it) count += __popcll(__ballot(s.id[it] == e));
+  for (int it = 0; it < kScanIters; ++it)
+    count += __popcll(__ballot(s.id[it] == e && s.begin + it * kWave + lane < s.end));
   if (lane == 0) wave_count[wave] = count;
   __syncthreads();
   int offset = 0, total = 0;
@@ -94,7 +104,7 @@ __device__ int scan_ids(const ScanIds &s, int e, int *list, int *wave_count) {
   }
 #pragma unroll
   for (int it = 0; it < kScanIters; ++it) {
-    const bool hit = s.id[it] == e;
+    const bool hit = s.id[it] == e && s.begin + it * kWave + lane < s.end;
     const uint64_t mask = __ballot(hit);
     const int slot = offset + __popcll(mask & below);
     if (hit && slot < kMaxScanRows) list[slot] = s.begin + it * kWave + lane;
@@ -115,12 +125,13 @@ struct RouteSet {
 
 // KS: 32-wide k steps per wave, hidden = KS * 32 * kWaves. Column tile of 16
 // gate rows and the matching 16 up rows.
-template <int KS, bool kScan>
+template <int KS, int kMode>
 __global__ void __launch_bounds__(kThreads)
 gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
                const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
                const int32_t *__restrict__ ids, int routes, int topk, int hidden, int inter,
-               int experts, int bm, int prefetch, bf16 *__restrict__ act) {
+               int experts, int bm, bf16 *__restrict__ act) {
+  constexpr bool kScan = kMode != kBlocks;
   __shared__ float red[kWaves][2][4][kWave];
   __shared__ int list[kScan ? kMaxScanRows : 1];
   __shared__ int wave_count[kWaves];
@@ -142,12 +153,16 @@ gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
   if constexpr (kScan) {
     const int e = blockIdx.y;
     const ScanIds scan = load_ids(ids, routes);
-    __builtin_amdgcn_sched_barrier(0);  // keep the ids loads ahead of the weights
-    if (prefetch) load_weights(e);
+    // The ids loads stay ahead of the weights, so the scan waits for them
+    // only (vector loads complete in issue order). A compile-time choice: a
+    // runtime branch around the prefetch would leave the scan's wait count
+    // to the path without it, i.e. waiting for the weights too.
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kMode == kScanPrefetch) load_weights(e);
     __builtin_amdgcn_sched_barrier(0);
     const int n = scan_ids(scan, e, list, wave_count);
     if (n == 0) return;
-    if (!prefetch) load_weights(e);
+    if constexpr (kMode == kScanLazy) load_weights(e);
     set = RouteSet{nullptr, list, 0, n};
   } else {
     int e, r0, r1;
@@ -197,12 +212,13 @@ gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
 
 // KS: 32-wide k steps per wave, inter = KS * 32 * kWaves. Column tile of 32
 // (two MFMA tiles).
-template <int KS, bool kScan>
+template <int KS, int kMode>
 __global__ void __launch_bounds__(kThreads)
 down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
             const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
             const int32_t *__restrict__ ids, int routes, int hidden, int inter, int experts, int bm,
-            int prefetch, bf16 *__restrict__ y) {
+            bf16 *__restrict__ y) {
+  constexpr bool kScan = kMode != kBlocks;
   __shared__ float red[kWaves][2][4][kWave];
   __shared__ int list[kScan ? kMaxScanRows : 1];
   __shared__ int wave_count[kWaves];
@@ -224,12 +240,16 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
   if constexpr (kScan) {
     const int e = blockIdx.y;
     const ScanIds scan = load_ids(ids, routes);
-    __builtin_amdgcn_sched_barrier(0);  // keep the ids loads ahead of the weights
-    if (prefetch) load_weights(e);
+    // The ids loads stay ahead of the weights, so the scan waits for them
+    // only (vector loads complete in issue order). A compile-time choice: a
+    // runtime branch around the prefetch would leave the scan's wait count
+    // to the path without it, i.e. waiting for the weights too.
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kMode == kScanPrefetch) load_weights(e);
     __builtin_amdgcn_sched_barrier(0);
     const int n = scan_ids(scan, e, list, wave_count);
     if (n == 0) return;
-    if (!prefetch) load_weights(e);
+    if constexpr (kMode == kScanLazy) load_weights(e);
     set = RouteSet{nullptr, list, 0, n};
   } else {
     int e, r0, r1;
@@ -294,7 +314,9 @@ bool ks_ok(int64_t n) {
 
 // Weight tiles are prefetched before the route scan when an empty expert is
 // unlikely (>= 4 routes per expert on average).
-int prefetch_flag(int64_t routes, int64_t experts) { return routes >= 4 * experts; }
+int route_mode(bool scan, int64_t routes, int64_t experts) {
+  return !scan ? kBlocks : (routes >= 4 * experts ? kScanPrefetch : kScanLazy);
+}
 
 }  // namespace
 
@@ -321,16 +343,19 @@ int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const
   const int64_t gy = scan ? experts : cdiv(routes, bm) + experts;
   if (gy > 65535) return LM_EUNSUPPORTED;
   const dim3 grid((unsigned)(inter / 16), (unsigned)gy);
-  const int pf = prefetch_flag(routes, experts);
+  const int mode = route_mode(scan, routes, experts);
   switch (hidden / 128) {
 #define X(KS)                                                                                   \
   case KS:                                                                                      \
-    if (scan)                                                                                   \
-      gate_up_kernel<KS, true><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, ids,     \
-          (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, pf, act);          \
+    if (mode == kScanPrefetch)                                                                  \
+      gate_up_kernel<KS, kScanPrefetch><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, \
+          ids, (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, act);         \
+    else if (mode == kScanLazy)                                                                 \
+      gate_up_kernel<KS, kScanLazy><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted,     \
+          ids, (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, act);         \
     else                                                                                        \
-      gate_up_kernel<KS, false><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, ids,    \
-          (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, pf, act);          \
+      gate_up_kernel<KS, kBlocks><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, ids,  \
+          (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, act);              \
     break;
     LM_KS_LIST(X)
 #undef X
@@ -350,16 +375,19 @@ int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const i
   const int64_t gy = scan ? experts : cdiv(routes, bm) + experts;
   if (gy > 65535) return LM_EUNSUPPORTED;
   const dim3 grid((unsigned)(hidden / 32), (unsigned)gy);
-  const int pf = prefetch_flag(routes, experts);
+  const int mode = route_mode(scan, routes, experts);
   switch (inter / 128) {
 #define X(KS)                                                                                  \
   case KS:                                                                                     \
-    if (scan)                                                                                  \
-      down_kernel<KS, true><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids,      \
-          (int)routes, (int)hidden, (int)inter, (int)experts, bm, pf, y);                      \
+    if (mode == kScanPrefetch)                                                                 \
+      down_kernel<KS, kScanPrefetch><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted,  \
+          ids, (int)routes, (int)hidden, (int)inter, (int)experts, bm, y);                     \
+    else if (mode == kScanLazy)                                                                \
+      down_kernel<KS, kScanLazy><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids, \
+          (int)routes, (int)hidden, (int)inter, (int)experts, bm, y);                          \
     else                                                                                       \
-      down_kernel<KS, false><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids,     \
-          (int)routes, (int)hidden, (int)inter, (int)experts, bm, pf, y);                      \
+      down_kernel<KS, kBlocks><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids,   \
+          (int)routes, (int)hidden, (int)inter, (int)experts, bm, y);                          \
     break;
     LM_KS_LIST(X)
 #undef X
