@@ -210,6 +210,76 @@ gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
   }
 }
 
+
+// The decode scan path with the weight tile prefetched (kScanPrefetch), as a
+// kernel of its own: activation rows past the route set repeat its last
+// route (unconditional loads; MFMA rows are independent and those outputs
+// are never stored), and a set of at most 16 routes -- the common case --
+// runs without the row-block loop. That keeps a wave within 128 registers up
+// to hidden 1536, so four workgroups share a CU: 1024 of the decode step's
+// 1280 weight tiles (Granite-3B shape) are in flight at once instead of 768.
+template <int KS>
+__global__ void __launch_bounds__(kThreads, KS <= 12 ? 4 : 2)
+gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
+                    const int32_t *__restrict__ ids, int routes, int topk, int hidden, int inter,
+                    bf16 *__restrict__ act) {
+  __shared__ float red[kWaves][2][4][kWave];
+  __shared__ int list[kMaxScanRows];
+  __shared__ int wave_count[kWaves];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int col = lane % 16, grp = lane / 16;
+  const int e = blockIdx.y, n0 = blockIdx.x * 16;
+  const int kbase = wave * KS * 32 + grp * 8;
+  const bf16 *wg = w13 + ((int64_t)e * 2 * inter + n0 + col) * hidden + kbase;
+  const bf16 *wu = wg + (int64_t)inter * hidden;
+  u32x4 bg[KS], bu[KS], a[KS];
+  const ScanIds scan = load_ids(ids, routes);
+  __builtin_amdgcn_sched_barrier(0);  // ids first: the scan waits for them only
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    bg[s] = load16(wg + s * 32);
+    bu[s] = load16(wu + s * 32);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int n = scan_ids(scan, e, list, wave_count);
+  if (n == 0) return;
+  auto block = [&](int rb) {
+    const bf16 *xr = x + (int64_t)(list[min(rb + col, n - 1)] / topk) * hidden + kbase;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) a[s] = load16(xr + s * 32);
+    f32x4 cg = {0.f, 0.f, 0.f, 0.f}, cu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      cg = mfma16x16x32(a[s], bg[s], cg);
+      cu = mfma16x16x32(a[s], bu[s], cu);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[wave][0][i][lane] = cg[i];
+      red[wave][1][i][lane] = cu[i];
+    }
+    __syncthreads();
+    // Wave w finishes C row 4*grp + w of every lane group.
+    float g = 0.f, u = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      g += red[w][0][wave][lane];
+      u += red[w][1][wave][lane];
+    }
+    const int row = rb + grp * 4 + wave;
+    if (row < n) {
+      const float h = round_bf16(silu(round_bf16(g))) * round_bf16(u);
+      act[(int64_t)list[row] * inter + n0 + col] = (bf16)f32_to_bf16(h);
+    }
+    __syncthreads();
+  };
+  if (n <= 16) {
+    block(0);
+  } else {
+    for (int rb = 0; rb < n; rb += 16) block(rb);
+  }
+}
+
 // KS: 32-wide k steps per wave, inter = KS * 32 * kWaves. Column tile of 32
 // (two MFMA tiles).
 template <int KS, int kMode>
@@ -348,8 +418,8 @@ int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const
 #define X(KS)                                                                                   \
   case KS:                                                                                      \
     if (mode == kScanPrefetch)                                                                  \
-      gate_up_kernel<KS, kScanPrefetch><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, \
-          ids, (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, act);         \
+      gate_up_scan_kernel<KS><<<grid, kThreads, 0, stream>>>(x, w13, ids, (int)routes,          \
+          (int)topk, (int)hidden, (int)inter, act);                                             \
     else if (mode == kScanLazy)                                                                 \
       gate_up_kernel<KS, kScanLazy><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted,     \
           ids, (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, act);         \
