@@ -262,10 +262,10 @@ def main():
                                 f"{args.new_tokens} new tokens, greedy, one hipGraph per decode step"),
                    "global_batch": args.batch, "seq_len": args.prompt, "new_tokens": args.new_tokens,
                    "capacity": engine.capacity, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "gate_up_kernel (lm_moe_gate_up)",
+        "roofline": {"bound": "hbm", "kernel": "gate_up_scan_kernel (lm_moe_gate_up)",
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("gate_up_kernel.granite3b_b64_decode.txt"),
+                     "traffic": measured_traffic("gate_up_scan_kernel.granite3b_b64_decode.txt"),
                      "bytes_per_launch": int(roof["gate_up_bytes"]), "us_per_launch": round(roof["gate_up_us"], 2),
                      "active_experts": roof["active"]},
         "fused_moe": {"achieved": round(fused_gbs, 1), "unit": "GB/s", "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
