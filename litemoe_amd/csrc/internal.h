@@ -27,4 +27,24 @@ int pick_block_rows(int64_t block_rows, int64_t tokens);
 
 inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
+// router.hip: the stable argsort of lm_moe_align. Above kAlignChunkedMinRoutes
+// routes it runs over 1024-route chunks in three launches, given a scratch
+// of align_scratch_bytes (else one workgroup).
+constexpr int64_t kAlignChunkedMinRoutes = 8192;
+int64_t align_scratch_bytes(int64_t routes, int64_t local_experts);
+int launch_align(const int32_t *ids, int64_t routes, int64_t first_expert, int64_t local_experts,
+                 int32_t *offsets, int32_t *sorted, int32_t *inverse, int32_t *scratch,
+                 int64_t scratch_bytes, hipStream_t stream);
+
+// expert_gemm.hip: LDS-tiled MFMA GEMMs over lm_moe_align's 128-route
+// blocks, for prefill-sized route counts (act and y in route order).
+constexpr int64_t kExpertGemmMinRoutes = 4096;
+bool expert_gemm_ok(int64_t routes, int64_t hidden, int64_t inter);
+int launch_expert_gemm_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets,
+                               const int32_t *sorted, int64_t routes, int64_t topk, int64_t hidden,
+                               int64_t inter, int64_t experts, bf16 *act, hipStream_t stream);
+int launch_expert_gemm_down(const bf16 *act, const bf16 *w2, const int32_t *offsets,
+                            const int32_t *sorted, int64_t routes, int64_t hidden, int64_t inter,
+                            int64_t experts, bf16 *y, hipStream_t stream);
+
 }  // namespace lm

@@ -474,13 +474,15 @@ using namespace lm;
 
 namespace {
 struct ExpertWorkspace {
-  int32_t *offsets, *sorted;
+  int32_t *offsets, *sorted, *align_scratch;
+  int64_t align_bytes;
   bf16 *act, *y;
   int64_t bytes;
 };
 
-// Layout: offsets [E+1], sorted [R] (block path only), act [R, I], and (for
-// lm_fused_experts) y [R, H].
+// Layout: offsets [E+1], sorted [R] (block path only), the chunked align's
+// counts and bases (large R only), act [R, I], and (for lm_fused_experts)
+// y [R, H].
 ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, int64_t inter,
                       int64_t experts, bool with_y) {
   const int64_t routes = tokens * topk;
@@ -491,6 +493,9 @@ ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, 
   off += align_up(4 * (experts + 1), 256);
   w.sorted = reinterpret_cast<int32_t *>(p + off);
   off += align_up(4 * routes, 256);
+  w.align_scratch = reinterpret_cast<int32_t *>(p + off);
+  w.align_bytes = align_scratch_bytes(routes, experts);
+  off += align_up(w.align_bytes, 256);
   w.act = reinterpret_cast<bf16 *>(p + off);
   off += align_up(2 * routes * inter, 256);
   w.y = with_y ? reinterpret_cast<bf16 *>(p + off) : nullptr;
@@ -513,8 +518,16 @@ int run_routes(const void *x, const void *w13, const void *w2, const int32_t *to
                        experts, 0, y, s);
   }
   const int bm = pick_block_rows(block_rows, tokens);
-  int rc = lm_moe_align(topk_ids, routes, 0, experts, w.offsets, w.sorted, nullptr, stream);
+  int rc = launch_align(topk_ids, routes, 0, experts, w.offsets, w.sorted, nullptr,
+                        w.align_scratch, w.align_bytes, s);
   if (rc) return rc;
+  if (block_rows == 0 && expert_gemm_ok(routes, hidden, inter)) {
+    rc = launch_expert_gemm_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, routes,
+                                    topk, hidden, inter, experts, w.act, s);
+    if (rc) return rc;
+    return launch_expert_gemm_down(w.act, (const bf16 *)w2, w.offsets, w.sorted, routes, hidden,
+                                   inter, experts, y, s);
+  }
   rc = launch_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, nullptr, routes,
                       topk, hidden, inter, experts, bm, w.act, s);
   if (rc) return rc;
@@ -546,6 +559,10 @@ extern "C" int lm_moe_gate_up(const void *x, const void *w13, const int32_t *exp
   if (topk_ids && !scan_path(routes / topk, topk)) return LM_EUNSUPPORTED;
   if (routes == 0) return LM_OK;
   LM_REQUIRE(x && w13 && act && (topk_ids || (expert_offsets && sorted_routes)));
+  if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter))
+    return launch_expert_gemm_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets,
+                                      sorted_routes, routes, topk, hidden, inter, experts,
+                                      (bf16 *)act, (hipStream_t)stream);
   return launch_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets, sorted_routes, topk_ids,
                         routes, topk, hidden, inter, experts, pick_block_rows(block_rows, routes),
                         (bf16 *)act, (hipStream_t)stream);
@@ -560,6 +577,10 @@ extern "C" int lm_moe_down(const void *act, const void *w2, const int32_t *exper
   if (topk_ids && routes > kWaves * kScanIters * kWave) return LM_EUNSUPPORTED;
   if (routes == 0) return LM_OK;
   LM_REQUIRE(act && w2 && y && (topk_ids || (expert_offsets && sorted_routes)));
+  if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter))
+    return launch_expert_gemm_down((const bf16 *)act, (const bf16 *)w2, expert_offsets,
+                                   sorted_routes, routes, hidden, inter, experts, (bf16 *)y,
+                                   (hipStream_t)stream);
   return launch_down((const bf16 *)act, (const bf16 *)w2, expert_offsets, sorted_routes, topk_ids,
                      routes, hidden, inter, experts, pick_block_rows(block_rows, routes), (bf16 *)y,
                      (hipStream_t)stream);

@@ -6,7 +6,7 @@
 // Weights follow vLLM fused_topk / HF GraniteMoeTopKRouter: softmax over the
 // k selected logits (renormalize) or over all E logits.
 // References: litemoe/model.py:110-118, ops.py:7-12, ops.py:163-173.
-#include "common.h"
+#include "internal.h"
 
 namespace lm {
 namespace {
@@ -570,6 +570,91 @@ align_kernel(const int32_t *__restrict__ ids, int routes, int first, int local,
   }
 }
 
+
+// The same stable argsort for large route counts, over chunks of 1024 routes
+// (16 waves x 64) in three launches: per-chunk key counts; one workgroup
+// turning them into key offsets and per-(chunk, key) bases (key-major, then
+// chunk order); and the scatter, each route to its chunk's base plus its rank
+// among equal keys earlier in the chunk. Every lane loads one id (clamped,
+// masked), so no wave waits on a chain of loads.
+constexpr int kChunk = 1024;
+
+template <bool kScatter>
+__global__ void __launch_bounds__(kChunk)
+align_chunk_kernel(const int32_t *__restrict__ ids, int routes, int first, int local,
+                   int32_t *__restrict__ counts, const int32_t *__restrict__ bases,
+                   int32_t *__restrict__ sorted, int32_t *__restrict__ inverse) {
+  extern __shared__ int wave_cnt[];  // [kAlignWaves][keys]
+  const int keys = local + 1;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  for (int i = threadIdx.x; i < kAlignWaves * keys; i += kChunk) wave_cnt[i] = 0;
+  const int r = blockIdx.x * kChunk + threadIdx.x;
+  const bool valid = r < routes;
+  const int e = ids[min(r, routes - 1)] - first;
+  const int key = valid && e >= 0 && e < local ? e : local;
+  const uint64_t eq = match_key(key, valid, 32 - __clz(local));
+  const uint64_t below = (1ull << lane) - 1ull;
+  __syncthreads();
+  if (valid && (eq & below) == 0ull) wave_cnt[wave * keys + key] = __popcll(eq);
+  __syncthreads();
+  if constexpr (!kScatter) {
+    if (threadIdx.x < keys) {
+      int total = 0;
+#pragma unroll
+      for (int w = 0; w < kAlignWaves; ++w) total += wave_cnt[w * keys + threadIdx.x];
+      counts[(int64_t)blockIdx.x * keys + threadIdx.x] = total;
+    }
+  } else {
+    if (threadIdx.x < keys) {
+      int running = bases[(int64_t)blockIdx.x * keys + threadIdx.x];
+#pragma unroll
+      for (int w = 0; w < kAlignWaves; ++w) {
+        const int c = wave_cnt[w * keys + threadIdx.x];
+        wave_cnt[w * keys + threadIdx.x] = running;
+        running += c;
+      }
+    }
+    __syncthreads();
+    if (valid) {
+      const int pos = wave_cnt[wave * keys + key] + __popcll(eq & below);
+      sorted[pos] = r;
+      if (inverse) inverse[r] = pos;
+    }
+  }
+}
+
+// One workgroup: offsets[k] = routes with a smaller key; bases[c][k] =
+// offsets[k] + routes of key k in chunks before c.
+__global__ void __launch_bounds__(kAlignThreads)
+align_scan_kernel(const int32_t *__restrict__ counts, int chunks, int keys,
+                  int32_t *__restrict__ bases, int32_t *__restrict__ offsets) {
+  __shared__ int scan[2][kAlignThreads];
+  const int k = threadIdx.x;
+  int total = 0;
+  if (k < keys) {
+#pragma unroll 8
+    for (int c = 0; c < chunks; ++c) total += counts[(int64_t)c * keys + k];
+  }
+  scan[0][k] = k < keys ? total : 0;
+  __syncthreads();
+  int src = 0;
+  for (int d = 1; d < kAlignThreads; d <<= 1) {
+    scan[1 - src][k] = scan[src][k] + (k >= d ? scan[src][k - d] : 0);
+    src = 1 - src;
+    __syncthreads();
+  }
+  if (k < keys) {
+    int running = scan[src][k] - total;  // exclusive
+    offsets[k] = running;
+#pragma unroll 8
+    for (int c = 0; c < chunks; ++c) {
+      const int v = counts[(int64_t)c * keys + k];
+      bases[(int64_t)c * keys + k] = running;
+      running += v;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace lm
 
@@ -670,16 +755,42 @@ extern "C" int lm_topk_softmax(const void *logits, int64_t tokens, int64_t exper
   return LM_OK;
 }
 
+namespace lm {
+
+int64_t align_scratch_bytes(int64_t routes, int64_t local_experts) {
+  return routes > kAlignChunkedMinRoutes ? 2 * 4 * cdiv(routes, kChunk) * (local_experts + 1) : 0;
+}
+
+int launch_align(const int32_t *ids, int64_t routes, int64_t first_expert, int64_t local_experts,
+                 int32_t *offsets, int32_t *sorted, int32_t *inverse, int32_t *scratch,
+                 int64_t scratch_bytes, hipStream_t stream) {
+  const int keys = (int)local_experts + 1;
+  const size_t wave_bytes = sizeof(int) * (size_t)kAlignWaves * keys;
+  const int64_t need = align_scratch_bytes(routes, local_experts);
+  if (need > 0 && scratch && scratch_bytes >= need) {
+    const int chunks = (int)cdiv(routes, kChunk);
+    int32_t *counts = scratch, *bases = scratch + (int64_t)chunks * keys;
+    align_chunk_kernel<false><<<chunks, kChunk, wave_bytes, stream>>>(
+        ids, (int)routes, (int)first_expert, (int)local_experts, counts, nullptr, nullptr, nullptr);
+    align_scan_kernel<<<1, kAlignThreads, 0, stream>>>(counts, chunks, keys, bases, offsets);
+    align_chunk_kernel<true><<<chunks, kChunk, wave_bytes, stream>>>(
+        ids, (int)routes, (int)first_expert, (int)local_experts, nullptr, bases, sorted, inverse);
+  } else {
+    align_kernel<<<1, kAlignThreads, wave_bytes + sizeof(int) * 2 * kAlignThreads, stream>>>(
+        ids, (int)routes, (int)first_expert, (int)local_experts, offsets, sorted, inverse);
+  }
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+}  // namespace lm
+
 extern "C" int lm_moe_align(const int32_t *ids, int64_t routes, int64_t first_expert,
                             int64_t local_experts, int32_t *expert_offsets, int32_t *sorted_routes,
                             int32_t *inverse, void *stream) {
   LM_REQUIRE(routes >= 0 && routes < (int64_t)1 << 30 && local_experts > 0 && first_expert >= 0);
   if (local_experts > kMaxAlignExperts) return LM_EUNSUPPORTED;
   LM_REQUIRE(expert_offsets && (routes == 0 || (ids && sorted_routes)));
-  const size_t shmem = sizeof(int) * ((size_t)kAlignWaves * (local_experts + 1) + 2 * kAlignThreads);
-  align_kernel<<<1, kAlignThreads, shmem, (hipStream_t)stream>>>(
-      ids, (int)routes, (int)first_expert, (int)local_experts, expert_offsets, sorted_routes,
-      inverse);
-  LM_CHECK_LAUNCH();
-  return LM_OK;
+  return launch_align(ids, routes, first_expert, local_experts, expert_offsets, sorted_routes,
+                      inverse, nullptr, 0, (hipStream_t)stream);
 }
