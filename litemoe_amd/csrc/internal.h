@@ -39,7 +39,7 @@ int launch_align(const int32_t *ids, int64_t routes, int64_t first_expert, int64
 // expert_gemm.hip: LDS-tiled MFMA GEMMs over lm_moe_align's 128-route
 // blocks, for prefill-sized route counts (act and y in route order).
 constexpr int64_t kExpertGemmMinRoutes = 4096;
-bool expert_gemm_ok(int64_t routes, int64_t hidden, int64_t inter);
+bool expert_gemm_ok(int64_t routes, int64_t hidden, int64_t inter, int64_t experts);
 int launch_expert_gemm_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets,
                                const int32_t *sorted, int64_t routes, int64_t topk, int64_t hidden,
                                int64_t inter, int64_t experts, bf16 *act, hipStream_t stream);

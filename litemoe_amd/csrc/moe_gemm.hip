@@ -521,7 +521,7 @@ int run_routes(const void *x, const void *w13, const void *w2, const int32_t *to
   int rc = launch_align(topk_ids, routes, 0, experts, w.offsets, w.sorted, nullptr,
                         w.align_scratch, w.align_bytes, s);
   if (rc) return rc;
-  if (block_rows == 0 && expert_gemm_ok(routes, hidden, inter)) {
+  if (block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts)) {
     rc = launch_expert_gemm_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, routes,
                                     topk, hidden, inter, experts, w.act, s);
     if (rc) return rc;
@@ -559,7 +559,7 @@ extern "C" int lm_moe_gate_up(const void *x, const void *w13, const int32_t *exp
   if (topk_ids && !scan_path(routes / topk, topk)) return LM_EUNSUPPORTED;
   if (routes == 0) return LM_OK;
   LM_REQUIRE(x && w13 && act && (topk_ids || (expert_offsets && sorted_routes)));
-  if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter))
+  if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts))
     return launch_expert_gemm_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets,
                                       sorted_routes, routes, topk, hidden, inter, experts,
                                       (bf16 *)act, (hipStream_t)stream);
@@ -577,7 +577,7 @@ extern "C" int lm_moe_down(const void *act, const void *w2, const int32_t *exper
   if (topk_ids && routes > kWaves * kScanIters * kWave) return LM_EUNSUPPORTED;
   if (routes == 0) return LM_OK;
   LM_REQUIRE(act && w2 && y && (topk_ids || (expert_offsets && sorted_routes)));
-  if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter))
+  if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts))
     return launch_expert_gemm_down((const bf16 *)act, (const bf16 *)w2, expert_offsets,
                                    sorted_routes, routes, hidden, inter, experts, (bf16 *)y,
                                    (hipStream_t)stream);
