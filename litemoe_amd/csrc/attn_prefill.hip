@@ -1,12 +1,17 @@
 // Packed variable-length (causal) attention on MFMA, head_dim 64.
 //
 // Workgroup (query block of 64, q head, sequence); wave w owns 16 queries.
-// Keys stream in tiles of 32 staged through LDS (K row-major, V transposed).
+// Keys stream in tiles of 32 staged through LDS, K and V both row-major; the
+// next tile is loaded into registers while the current one is computed.
 // Scores are computed transposed, S^T = K . Q^T, so each lane's C fragment
 // (keys 16h + 4*(l/16) + i, query l%16) is directly the A operand of P . V:
 // the eight keys a lane holds become the eight k slots of one
-// v_mfma_f32_16x16x32_bf16, and V^T in LDS supplies the matching B slots.
-// Online softmax (fp32) per query; P is rounded to bf16 for the MFMA.
+// v_mfma_f32_16x16x32_bf16. The matching B slots (four keys of one channel
+// per 64-bit half) come from row-major V through gfx950's transposing LDS
+// read, ds_read_b64_tr_b16: within each 16-lane group, lanes 4j..4j+3 point
+// at 16 consecutive channels of key row j, and lane p receives channel p of
+// rows 0..3. Online softmax (fp32, exp2 with the scale folded in) per query;
+// P is rounded to bf16 for the MFMA.
 //
 // Reference semantics: litemoe/packed.py:12-16 (aten varlen flash attention,
 // causal, q and k share cu_seqlens).
@@ -20,10 +25,21 @@ constexpr int kThreads = 256;
 constexpr int kBQ = 64;
 constexpr int kBK = 32;
 constexpr int kKPad = 8;
-constexpr int kVPad = 8;
 
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
+
+// Scores and running maxima in log2 units: scale * log2(e) is folded into
+// the q.k product, so each exponential is one v_exp_f32.
 __device__ __forceinline__ float factor(float m, float mnew) {
-  return m == -INFINITY ? 0.f : __expf(m - mnew);
+  return m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+}
+
+// Four bf16 of one channel from four key rows (see the header).
+__device__ __forceinline__ uint2 read_tr(const bf16 *p) {
+  const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)p);
+  return uint2{(uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16),
+               (uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16)};
 }
 
 __global__ void __launch_bounds__(kThreads)
@@ -32,7 +48,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
                const int32_t *__restrict__ cu, int q_heads, int kv_heads, float scale, int causal,
                bf16 *__restrict__ out) {
   __shared__ __attribute__((aligned(16))) bf16 ks_lds[kBK][kD + kKPad];
-  __shared__ __attribute__((aligned(16))) bf16 vt_lds[kD][kBK + kVPad];
+  __shared__ __attribute__((aligned(16))) bf16 vs_lds[kBK][kD + kKPad];
   const int qb = blockIdx.x, hq = blockIdx.y, seq = blockIdx.z;
   const int start = cu[seq];
   const int len = cu[seq + 1] - start;
@@ -43,6 +59,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
   const int col = lane % 16, grp = lane / 16;
   const int wq0 = q0 + wave * 16;
   const int qi = wq0 + col;  // this lane's query (softmax state owner)
+  const float sl2 = scale * 1.4426950408889634f;
 
   u32x4 qf0 = {0u, 0u, 0u, 0u}, qf1 = {0u, 0u, 0u, 0u};
   if (qi < len) {
@@ -57,22 +74,29 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
 
   const int kend = causal ? min(len, q0 + kBQ) : len;
   const bool wave_live = wq0 < len;
+  // Tile staging: thread -> (key skey, channels 8*sdc..+7). Keys past the
+  // sequence repeat its last key (finite values; their scores are masked).
   const int skey = threadIdx.x / 8, sdc = threadIdx.x % 8;
+  const bf16 *kbase = k + (int64_t)start * ks0 + (int64_t)hk * ks1 + sdc * 8;
+  const bf16 *vbase = v + (int64_t)start * vs0 + (int64_t)hk * vs1 + sdc * 8;
+  auto load = [&](int kt, u32x4 &kv, u32x4 &vv) {
+    const int64_t row = min(kt + skey, len - 1);
+    kv = *reinterpret_cast<const u32x4 *>(kbase + row * ks0);
+    vv = *reinterpret_cast<const u32x4 *>(vbase + row * vs0);
+  };
+  // Transposing-read addresses: lane 16g + 4j + t reads channels 4t..4t+3
+  // (plus 16 per channel block) of key row 4g + j (slots 0-3) or
+  // 16 + 4g + j (slots 4-7), matching the keys of the P fragment.
+  const int trow = 4 * grp + (col / 4), tch = 4 * (col % 4);
+  u32x4 kv, vv;
+  load(0, kv, vv);
   for (int kt = 0; kt < kend; kt += kBK) {
-    u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-    if (kt + skey < len) {
-      const int64_t row = start + kt + skey;
-      kv = *reinterpret_cast<const u32x4 *>(k + row * ks0 + (int64_t)hk * ks1 + sdc * 8);
-      vv = *reinterpret_cast<const u32x4 *>(v + row * vs0 + (int64_t)hk * vs1 + sdc * 8);
-    }
-    __syncthreads();
+    __syncthreads();  // the previous tile is no longer read
     *reinterpret_cast<u32x4 *>(&ks_lds[skey][sdc * 8]) = kv;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      vt_lds[sdc * 8 + 2 * i][skey] = (bf16)(vv[i] & 0xffffu);
-      vt_lds[sdc * 8 + 2 * i + 1][skey] = (bf16)(vv[i] >> 16);
-    }
+    *reinterpret_cast<u32x4 *>(&vs_lds[skey][sdc * 8]) = vv;
     __syncthreads();
+    // The next tile streams in while this one is computed.
+    load(min(kt + kBK, kend - 1), kv, vv);
     if (!wave_live || (causal && kt > wq0 + 15)) continue;
     f32x4 st[2];
 #pragma unroll
@@ -82,6 +106,9 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
       st[h] = mfma16x16x32(a0, qf0, f32x4{0.f, 0.f, 0.f, 0.f});
       st[h] = mfma16x16x32(a1, qf1, st[h]);
     }
+    // Only a tile past the sequence end or crossing the causal diagonal of
+    // this wave's queries has masked scores.
+    const bool masking = kt + kBK > len || (causal && kt + kBK - 1 > wq0);
     float s[2][4];
     float mt = -INFINITY;
 #pragma unroll
@@ -89,8 +116,8 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = kt + 16 * h + grp * 4 + i;
-        const bool masked = j >= len || (causal && j > qi);
-        s[h][i] = masked ? -INFINITY : st[h][i] * scale;
+        const bool masked = masking && (j >= len || (causal && j > qi));
+        s[h][i] = masked ? -INFINITY : st[h][i] * sl2;
         mt = fmaxf(mt, s[h][i]);
       }
     mt = fmaxf(mt, shfl_xor(mt, 16));
@@ -104,7 +131,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p[i] = s[h][i] == -INFINITY ? 0.f : __expf(s[h][i] - mn);
+        p[i] = __builtin_amdgcn_exp2f(s[h][i] - mn);  // exp2(-inf) = 0; mn is finite
         rs += p[i];
       }
       pw[2 * h] = pack_bf16(p[0], p[1]);
@@ -115,17 +142,21 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     l = l * corr + rs;
     m = mn;
     const u32x4 pa = {pw[0], pw[1], pw[2], pw[3]};
-    // O rows held by this lane are queries 4*grp + i of the wave.
-    float rc[4];
+    // O rows held by this lane are queries 4*grp + i of the wave; the
+    // rescale is skipped when no query of the wave moved its maximum.
+    if (__ballot(corr != 1.f)) {
+      float rc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rc[i] = __shfl(corr, grp * 4 + i, kWave);
+      for (int i = 0; i < 4; ++i) rc[i] = __shfl(corr, grp * 4 + i, kWave);
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[d][i] *= rc[i];
+    }
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[d][i] *= rc[i];
-      const bf16 *vr = &vt_lds[d * 16 + col][0];
-      const uint2 lo = *reinterpret_cast<const uint2 *>(vr + grp * 4);
-      const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16 + grp * 4);
+      const uint2 lo = read_tr(&vs_lds[trow][d * 16 + tch]);
+      const uint2 hi = read_tr(&vs_lds[16 + trow][d * 16 + tch]);
       const u32x4 vb = {lo.x, lo.y, hi.x, hi.y};
       o[d] = mfma16x16x32(pa, vb, o[d]);
     }
