@@ -109,20 +109,25 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     // Only a tile past the sequence end or crossing the causal diagonal of
     // this wave's queries has masked scores.
     const bool masking = kt + kBK > len || (causal && kt + kBK - 1 > wq0);
-    float s[2][4];
+    if (masking) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = kt + 16 * h + grp * 4 + i;
+          if (j >= len || (causal && j > qi)) st[h][i] = -INFINITY;
+        }
+    }
+    // The maximum is taken on the raw dot products (the scale is positive),
+    // and exp2(s * scale*log2e - m) is one FMA and one v_exp_f32.
     float mt = -INFINITY;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = kt + 16 * h + grp * 4 + i;
-        const bool masked = masking && (j >= len || (causal && j > qi));
-        s[h][i] = masked ? -INFINITY : st[h][i] * sl2;
-        mt = fmaxf(mt, s[h][i]);
-      }
+      for (int i = 0; i < 4; ++i) mt = fmaxf(mt, st[h][i]);
     mt = fmaxf(mt, shfl_xor(mt, 16));
     mt = fmaxf(mt, shfl_xor(mt, 32));
-    const float mn = fmaxf(m, mt);
+    const float mn = fmaxf(m, mt * sl2);
     const float corr = factor(m, mn);
     float rs = 0.f;
     uint32_t pw[4];
@@ -131,7 +136,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(s[h][i] - mn);  // exp2(-inf) = 0; mn is finite
+        p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[h][i], sl2, -mn));  // exp2(-inf) = 0; mn is finite
         rs += p[i];
       }
       pw[2 * h] = pack_bf16(p[0], p[1]);
