@@ -101,41 +101,62 @@ __device__ void select_topk(const float *logit, int experts, int topk, int renor
   }
 }
 
-// select_topk for experts <= 64, run by wave 0 alone with no LDS round trip
-// or barrier: logits are bf16, so (orderable bf16 bits, ~id) fits a 32-bit
-// key; lane e holds expert e's key and counts the larger keys broadcast with
-// readlane; the lane of each rank is found with a ballot. The selection, the
-// weights and the order of the softmax denominator's sum are those of
-// select_topk. The caller synchronises before (logits in LDS).
-__device__ void select_topk_wave(const float *logit, int experts, int topk, int renormalize,
+// select_topk for experts <= 64, run by wave 0 alone with no barrier: logits
+// are bf16, so (orderable bf16 bits, ~id) fits a 32-bit key. Lane e computes
+// expert e's key, publishes it to LDS and counts the larger keys among all
+// 64 read back as broadcasts (every lane reads the same address: no readlane
+// chain); the lane of rank 0 is found with a ballot, and the softmax terms of
+// the selection are summed in rank order through LDS. logit[kWave, 3*kWave)
+// is scratch. The selection, the weights and the order of the softmax
+// denominator's sum are those of select_topk. The caller synchronises before
+// (logits in LDS).
+__device__ __forceinline__ uint32_t select_key32(float v, int id) {
+  uint32_t h = __float_as_uint(v) >> 16;  // exact: logits are bf16 values
+  if ((h & 0x7fffu) > 0x7f80u) h = 0x7fc0u;
+  const uint32_t ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+  return (ord << 16) | (0xffffu - (uint32_t)id);
+}
+
+__device__ void select_topk_wave(float *logit, int experts, int topk, int renormalize,
                                  float *__restrict__ tw, int32_t *__restrict__ tid) {
   const int t = threadIdx.x;
   if (t >= kWave) return;
-  uint32_t key = 0u;  // below every real key
-  float v = 0.f;
-  if (t < experts) {
-    v = logit[t];
-    uint32_t h = __float_as_uint(v) >> 16;  // exact: logits are bf16 values
-    if ((h & 0x7fffu) > 0x7f80u) h = 0x7fc0u;
-    const uint32_t ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
-    key = (ord << 16) | (0xffffu - (uint32_t)t);
-  }
+  const float v = logit[min(t, experts - 1)];
+  const uint32_t key = t < experts ? select_key32(v, t) : 0u;  // 0: below every real key
+  // Each lane publishes its key once; every lane then compares against all
+  // 64 (broadcast reads, padding keys are 0 and never larger).
+  uint32_t *keys = reinterpret_cast<uint32_t *>(logit + kWave);
+  float *terms = logit + 2 * kWave;
+  keys[t] = key;
   int rank = 0;
-  for (int e = 0; e < experts; ++e)
-    rank += (uint32_t)__builtin_amdgcn_readlane((int)key, e) > key;
+#pragma unroll
+  for (int e4 = 0; e4 < kWave / 4; ++e4) {
+    const uint4 k4 = *reinterpret_cast<const uint4 *>(keys + 4 * e4);
+    rank += (k4.x > key) + (k4.y > key) + (k4.z > key) + (k4.w > key);
+  }
   if (t >= experts) rank = kWave;
   const int top = __builtin_ctzll(__ballot(rank == 0));
   const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
   const float ex = expf(v - m);
   float denom = 0.f;
   if (renormalize) {
-    for (int r = 0; r < topk; ++r) {
-      const int at = __builtin_ctzll(__ballot(rank == r));
-      denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), at));
+    if (rank < topk) terms[rank] = ex;
+#pragma unroll
+    for (int r4 = 0; r4 < kMaxTopk / 4; ++r4) {
+      const float4 t4 = *reinterpret_cast<const float4 *>(terms + 4 * r4);
+      const float tv[4] = {t4.x, t4.y, t4.z, t4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) denom += 4 * r4 + i < topk ? tv[i] : 0.f;
     }
   } else {
-    for (int e = 0; e < experts; ++e)
-      denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), e));
+    if (t < experts) terms[t] = ex;
+#pragma unroll
+    for (int e4 = 0; e4 < kWave / 4; ++e4) {
+      const float4 t4 = *reinterpret_cast<const float4 *>(terms + 4 * e4);
+      const float tv[4] = {t4.x, t4.y, t4.z, t4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) denom += 4 * e4 + i < experts ? tv[i] : 0.f;
+    }
   }
   if (rank < topk) {
     tw[rank] = ex / denom;
@@ -145,7 +166,7 @@ __device__ void select_topk_wave(const float *logit, int experts, int topk, int 
 
 // Both selections end with the outputs written; neither needs a barrier
 // after it.
-__device__ __forceinline__ void select(const float *logit, int experts, int topk, int renormalize,
+__device__ __forceinline__ void select(float *logit, int experts, int topk, int renormalize,
                                        float *sel_val, int *sel_id, float *__restrict__ tw,
                                        int32_t *__restrict__ tid) {
   if (experts <= kWave)
@@ -160,7 +181,7 @@ router_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ wr, int hidde
               int topk, int renormalize, bf16 *__restrict__ logits_out, float *__restrict__ tw,
               int32_t *__restrict__ tid) {
   __shared__ u32x4 zs[kMaxNormVec * kRouterThreads];
-  __shared__ float logit[kMaxExperts];
+  __shared__ __align__(16) float logit[kMaxExperts];
   __shared__ float sel_val[kMaxTopk];
   __shared__ int sel_id[kMaxTopk];
   const int64_t row = blockIdx.x;
@@ -176,7 +197,7 @@ router_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ wr, int hidde
 __global__ void __launch_bounds__(kRouterThreads)
 topk_from_logits_kernel(const bf16 *__restrict__ logits, int experts, int topk, int renormalize,
                         float *__restrict__ tw, int32_t *__restrict__ tid) {
-  __shared__ float logit[kMaxExperts];
+  __shared__ __align__(16) float logit[kMaxExperts];
   __shared__ float sel_val[kMaxTopk];
   __shared__ int sel_id[kMaxTopk];
   const int64_t row = blockIdx.x;
@@ -195,7 +216,7 @@ add_norm_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float a
                        int renormalize, bf16 *__restrict__ logits_out, float *__restrict__ tw,
                        int32_t *__restrict__ tid) {
   __shared__ u32x4 zs[kMaxNormVec * kRouterThreads];
-  __shared__ float logit[kMaxExperts];
+  __shared__ __align__(16) float logit[kMaxExperts];
   __shared__ float red[kRouterWaves];
   __shared__ float sel_val[kMaxTopk];
   __shared__ int sel_id[kMaxTopk];
@@ -322,7 +343,7 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
   typedef FastRouter<NV> F;
   constexpr int nvec = F::kNvec, NN = F::kNorm;
   __shared__ u32x4 zs[nvec];
-  __shared__ float logit[kMaxExperts];
+  __shared__ __align__(16) float logit[kMaxExperts];
   __shared__ float red[kRouterWaves];
   __shared__ float sel_val[kMaxTopk];
   __shared__ int sel_id[kMaxTopk];
