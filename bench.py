@@ -20,6 +20,17 @@ Also reported on the same JSON line:
                 bounded sample of the same decode step, extrapolated;
   engine_decode_tps  the reference's own metric from Engine.generate()
                 (decode_tokens / decode_s with the async output ring).
+
+Two other workloads of the survey's measurement table print their own JSON
+line (not the driver's decode line):
+  --prefill       cfg 4: packed prefill of 48 prompts, lengths U{64..2048}
+                  (seed 2), on the 3B shape: prefill tok/s, and the MFMA
+                  utilisation of the prefill MoE (uniform routes and 50% of
+                  routes on 4 hot experts) and of the prefill attention at
+                  the same token counts;
+  --flash-decode  cfg 5: decode attention over B=128 rows with contexts
+                  U{1024..4096} (seed 3), capacity 4096, KV filled N(0,1):
+                  GB/s of the KV stream against 8 TB/s.
 """
 import argparse
 import json
@@ -56,6 +67,8 @@ def parse():
                     help="skip decode timing: run only the MoE kernel timing (for counter collection)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy a 256 MiB device buffer 3 times (FETCH/WRITE counter calibration)")
+    ap.add_argument("--prefill", action="store_true", help="cfg 4 packed prefill (own JSON line)")
+    ap.add_argument("--flash-decode", action="store_true", help="cfg 5 decode attention (own JSON line)")
     return ap.parse_args()
 
 
@@ -120,6 +133,130 @@ def moe_roofline(model, cfg, batch, reps):
                 gate_up_bytes=gate_up_bytes, fused_bytes=fused_bytes)
 
 
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def hip_time(fn, reps):
+    """Average milliseconds per call of ``fn`` on the current stream."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def prefill_bench(args):
+    """cfg 4: packed prefill on the 3B shape (one JSON line)."""
+    import torch
+
+    from litemoe_amd import experts, packed, synth
+    from litemoe_amd.config import preset
+    from litemoe_amd.engine import Request
+    from litemoe_amd.ep import ExpertParallel
+    from litemoe_amd.experts import HipFusedExperts
+    from litemoe_amd.model import Granite
+    from litemoe_amd.optimized import OptimizedEngine
+
+    dev = torch.device("cuda:0")
+    cfg = preset(args.model)
+    w = synth.granite_weights(cfg, seed=0, device=dev, method="torch")
+    lengths = synth.ragged_lengths(48, 64, 2048, 2)
+    tokens = sum(lengths)
+    ep = ExpertParallel(1, 0, tokens, cfg.hidden_size, cfg.num_experts_per_tok, torch.bfloat16, dev,
+                        HipFusedExperts())
+    model = Granite(cfg, w, ep, 4096)
+    prompts = synth.prompts(48, lengths, cfg.vocab_size, 1)
+    engine = OptimizedEngine(model, [Request(str(i), p, 2) for i, p in enumerate(prompts)], ignore_eos=True)
+    times = []
+    with torch.inference_mode():
+        for _ in range(4):
+            engine.reset()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            engine.prefill()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t)
+        elapsed = min(times[1:])
+        log(f"prefill of {tokens} tokens: {elapsed * 1e3:.1f} ms")
+
+        # The MoE and the attention of one layer at the same token counts.
+        H, I, E, k = cfg.hidden_size, cfg.intermediate_size, cfg.num_local_experts, cfg.num_experts_per_tok
+        gen = torch.Generator(device=dev).manual_seed(5)
+        z = torch.randn(tokens, H, device=dev, generator=gen).to(torch.bfloat16)
+        layer = model.w["layers"][0]
+        rng = torch.Generator().manual_seed(6)
+        uniform = torch.stack([torch.randperm(E, generator=rng)[:k] for _ in range(tokens)]).int().to(dev)
+        hot = torch.full((E,), 0.5 / (E - 4))
+        hot[:4] = 0.5 / 4
+        skewed = torch.multinomial(hot.expand(tokens, E), k, replacement=False, generator=rng).int().to(dev)
+        moe_flops = tokens * k * 6 * I * H
+        moe = {}
+        for name, ids in (("uniform", uniform), ("hot4_50pct", skewed)):
+            y = experts.moe_routes(z, layer["input_linear"], layer["output_linear"], ids)
+            ms = hip_time(lambda: experts.moe_routes(z, layer["input_linear"], layer["output_linear"], ids, y=y), 5)
+            moe[name] = {"ms_per_layer": round(ms, 3), "tflops": round(moe_flops / ms / 1e9, 1),
+                         "frac": round(moe_flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
+        hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, 64
+        q = torch.randn(tokens, hq, d, device=dev, generator=gen).to(torch.bfloat16)
+        kk = torch.randn(tokens, hkv, d, device=dev, generator=gen).to(torch.bfloat16)
+        vv = torch.randn(tokens, hkv, d, device=dev, generator=gen).to(torch.bfloat16)
+        ends = torch.tensor(lengths, dtype=torch.int32).cumsum(0, dtype=torch.int32)
+        cu = torch.cat((ends.new_zeros(1), ends)).to(dev)
+        ms = hip_time(lambda: packed.varlen_attention(q, kk, vv, cu, max(lengths), cfg.attention_multiplier), 5)
+        attn_flops = sum(n * (n + 1) // 2 for n in lengths) * hq * 4 * d
+    line = {
+        "metric": "prefill tok/s, Granite-3B-shape bf16, cfg4 packed prefill", "value": round(tokens / elapsed, 1),
+        "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights (seed 0), prompt ids (seed 1), lengths U{64..2048} (seed 2)",
+        "config": {"workload": f"cfg4 packed prefill: {args.model} shape, 48 prompts, {tokens} tokens",
+                   "tokens": tokens, "ms": round(elapsed * 1e3, 2)},
+        "moe_mfma": {"flops_per_layer": moe_flops, "peak_tflops": BF16_PEAK_TFLOPS, **moe},
+        "attention_mfma": {"flops_per_layer": attn_flops, "ms_per_layer": round(ms, 3),
+                           "tflops": round(attn_flops / ms / 1e9, 1),
+                           "frac": round(attn_flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4)},
+    }
+    print(json.dumps(line), flush=True)
+
+
+def flash_decode_bench(args):
+    """cfg 5: decode attention, B=128, contexts U{1024..4096} (one JSON line)."""
+    import numpy as np
+    import torch
+
+    from litemoe_amd.flash_decode import FlashDecode
+
+    dev = torch.device("cuda:0")
+    batch, hq, hkv, d, cap = 128, 24, 8, 64, 4096
+    used_list = np.random.RandomState(3).randint(1024, 4097, size=batch)
+    used = torch.tensor(used_list, dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(8)
+    k = torch.randn(batch, hkv, cap, d, device=dev, generator=gen).to(torch.bfloat16)
+    v = torch.randn(batch, hkv, cap, d, device=dev, generator=gen).to(torch.bfloat16)
+    q = torch.randn(batch, hq, 1, d, device=dev, generator=gen).to(torch.bfloat16)
+    flash = FlashDecode(batch, hkv, hq // hkv, cap, dev, int(used_list.max()))
+    zeros = torch.zeros(batch, dtype=torch.int64, device=dev)
+    active = torch.ones(batch, dtype=torch.bool, device=dev)
+    with torch.inference_mode():
+        ms = hip_time(lambda: flash(q, k, v, zeros, active, 0.125, used=used), 20)
+    kv_bytes = int(used_list.sum()) * hkv * d * 2 * 2 + batch * hq * d * 2 * 2
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "flash-decode GB/s, cfg5 (B=128, ctx U{1024..4096})", "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "higher_is_better": True, "dtype": "bf16", "data": "synthetic: KV N(0,1) (seed 8), contexts seed 3",
+        "config": {"workload": "cfg5 decode attention, one layer", "batch": batch, "q_heads": hq, "kv_heads": hkv,
+                   "capacity": cap, "splits": flash.splits},
+        "us_per_layer": round(ms * 1e3, 2), "bytes_per_layer": kv_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def cpu_baseline(model, cfg, engine, state, layers, batch):
     """Time the CPU oracle's decode step on ``layers`` of the model's layers
     (weights and filled KV cache copied from the GPU), extrapolate to all."""
@@ -177,6 +314,11 @@ def main():
         torch.cuda.synchronize()
         log("copied 3 x 256 MiB")
         return
+
+    if args.prefill:
+        return prefill_bench(args)
+    if args.flash_decode:
+        return flash_decode_bench(args)
 
     from litemoe_amd import synth
     from litemoe_amd.config import preset
