@@ -24,17 +24,23 @@ __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w <
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // Round-to-nearest-even float -> bf16, NaN -> canonical quiet NaN 0x7fc0
-// (the conversion torch performs).
+// (c10::BFloat16's scalar conversion; torch's vectorised CPU conversion
+// differs only in writing 0xffff for NaN). gfx950's v_cvt_pk_bf16_f32 rounds every
+// non-NaN input (denormals included) exactly so; for NaN it keeps sign and
+// payload, so NaN is replaced afterwards.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+  if (lo != lo) h = (h & 0xffff0000u) | 0x7fc0u;
+  if (hi != hi) h = (h & 0xffffu) | 0x7fc00000u;
+  return h;
+}
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t h = __builtin_bit_cast(uint16_t, (__bf16)f);
+  return f != f ? 0x7fc0u : h;
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
-}
 
 // Eight bf16 (one 16-byte word) to floats.
 __device__ __forceinline__ void unpack8(const u32x4 &w, float *f) {

@@ -109,7 +109,8 @@ __device__ void select_topk(const float *logit, int experts, int topk, int renor
 // the selection are summed in rank order through LDS. logit[kWave, 3*kWave)
 // is scratch. The selection, the weights and the order of the softmax
 // denominator's sum are those of select_topk. The caller synchronises before
-// (logits in LDS).
+// (logits in LDS). select_topk_lanes is the same selection for any one wave
+// of the workgroup, with its own 2*kWave floats of LDS scratch.
 __device__ __forceinline__ uint32_t select_key32(float v, int id) {
   uint32_t h = __float_as_uint(v) >> 16;  // exact: logits are bf16 values
   if ((h & 0x7fffu) > 0x7f80u) h = 0x7fc0u;
@@ -117,16 +118,15 @@ __device__ __forceinline__ uint32_t select_key32(float v, int id) {
   return (ord << 16) | (0xffffu - (uint32_t)id);
 }
 
-__device__ void select_topk_wave(float *logit, int experts, int topk, int renormalize,
-                                 float *__restrict__ tw, int32_t *__restrict__ tid) {
-  const int t = threadIdx.x;
-  if (t >= kWave) return;
+__device__ void select_topk_lanes(const float *logit, float *scratch, int t, int experts,
+                                  int topk, int renormalize, float *__restrict__ tw,
+                                  int32_t *__restrict__ tid) {
   const float v = logit[min(t, experts - 1)];
   const uint32_t key = t < experts ? select_key32(v, t) : 0u;  // 0: below every real key
   // Each lane publishes its key once; every lane then compares against all
   // 64 (broadcast reads, padding keys are 0 and never larger).
-  uint32_t *keys = reinterpret_cast<uint32_t *>(logit + kWave);
-  float *terms = logit + 2 * kWave;
+  uint32_t *keys = reinterpret_cast<uint32_t *>(scratch);
+  float *terms = scratch + kWave;
   keys[t] = key;
   int rank = 0;
 #pragma unroll
@@ -162,6 +162,13 @@ __device__ void select_topk_wave(float *logit, int experts, int topk, int renorm
     tw[rank] = ex / denom;
     tid[rank] = t;
   }
+}
+
+__device__ __forceinline__ void select_topk_wave(float *logit, int experts, int topk,
+                                                 int renormalize, float *__restrict__ tw,
+                                                 int32_t *__restrict__ tid) {
+  if (threadIdx.x >= kWave) return;
+  select_topk_lanes(logit, logit + kWave, threadIdx.x, experts, topk, renormalize, tw, tid);
 }
 
 // Both selections end with the outputs written; neither needs a barrier
@@ -496,6 +503,199 @@ void launch_fast_router(int nv, int64_t tokens, bf16 *x, const bf16 *a, float al
   }
 }
 
+// Prefill-sized router: a workgroup of four waves routes kBatchRows = 16
+// tokens, for experts <= 64 and hidden = 512 * NVL.
+//  1. (kNorm) Wave w normalises tokens 4w..4w+3 in turn, with the next
+//     token's loads in flight: lane l holds 16-byte words l + 64i (i < NVL),
+//     the words threads l + 64j of rmsnorm_kernel hold (word (l + 64j) +
+//     256v for i = j + 4v). The sum of squares is kept per j in that
+//     thread's order and reduced by wave_sum per j, then over j in order, so
+//     x and z are bitwise the unfused kernels'.
+//  2. The 16 rows of z (x when !kNorm) are read back as MFMA A operands and
+//     the gate rows as B operands (both from L2); wave w accumulates k-steps
+//     [w K/4, (w+1) K/4) of the 16 x 16*NT logits with
+//     v_mfma_f32_16x16x32_bf16, and the four partial tiles are summed in
+//     wave order through LDS and rounded to bf16 (and to logits_out).
+//  3. Wave w selects the top-k of tokens 4w..4w+3 (select_topk_lanes).
+// The logits accumulate in the matrix core's order rather than
+// router_gemv's, so a logit can differ from the GEMV kernels' by one bf16
+// ulp (as a BLAS GEMM's order can); the selection is exact given the
+// logits. All 16 rows must exist (the caller routes a tail of fewer tokens
+// with the per-token kernels).
+constexpr int kBatchRows = 16;
+constexpr int kBatchWaves = 4;
+constexpr int kBatchThreads = kBatchWaves * kWave;
+constexpr int kRowsPerWave = kBatchRows / kBatchWaves;
+#ifndef LM_BATCH_ROUTER_MIN_TOKENS
+#define LM_BATCH_ROUTER_MIN_TOKENS 1024
+#endif
+constexpr int64_t kBatchRouterMinTokens = LM_BATCH_ROUTER_MIN_TOKENS;
+constexpr int kBatchSteps = 4;  // k-steps whose operand loads are issued together
+
+template <int NVL, bool kAdd>
+__device__ __forceinline__ void batch_load_row(const bf16 *__restrict__ x,
+                                               const bf16 *__restrict__ a, int64_t row,
+                                               u32x4 (&xv)[NVL], u32x4 (&av)[NVL]) {
+  const int lane = threadIdx.x % kWave;
+  const u32x4 *xr = reinterpret_cast<const u32x4 *>(x) + row * NVL * kWave;
+  const u32x4 *ar = reinterpret_cast<const u32x4 *>(a) + row * NVL * kWave;
+#pragma unroll
+  for (int i = 0; i < NVL; ++i) {
+    xv[i] = xr[lane + i * kWave];
+    if constexpr (kAdd) av[i] = ar[lane + i * kWave];
+  }
+}
+
+template <int NVL, bool kAdd>
+__device__ __forceinline__ void batch_norm_row(bf16 *__restrict__ x, float alpha,
+                                               const u32x4 (&gv)[NVL], float eps,
+                                               bf16 *__restrict__ z, int64_t row,
+                                               const u32x4 (&xv)[NVL], const u32x4 (&av)[NVL]) {
+  constexpr int kJ = NVL < kRouterWaves ? NVL : kRouterWaves;
+  const int lane = threadIdx.x % kWave;
+  u32x4 *xr = reinterpret_cast<u32x4 *>(x) + row * NVL * kWave;
+  u32x4 *zr = reinterpret_cast<u32x4 *>(z) + row * NVL * kWave;
+  float xn[NVL][8];
+  float ss[kJ];
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) ss[j] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NVL; ++i) {
+    unpack8(xv[i], xn[i]);
+    if constexpr (kAdd) {
+      float g[8];
+      unpack8(av[i], g);
+      u32x4 o;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) xn[i][c] = round_bf16(xn[i][c] + alpha * g[c]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = pack_bf16(xn[i][2 * c], xn[i][2 * c + 1]);
+      xr[lane + i * kWave] = o;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ss[i % kRouterWaves] += xn[i][c] * xn[i][c];
+  }
+  float total = 0.f;
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) total += wave_sum(ss[j]);
+  const float scale = 1.0f / sqrtf(total / (float)(NVL * 512) + eps);
+#pragma unroll
+  for (int i = 0; i < NVL; ++i) {
+    float g[8];
+    unpack8(gv[i], g);
+    u32x4 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      o[c] = pack_bf16(round_bf16(xn[i][2 * c] * scale) * g[2 * c],
+                       round_bf16(xn[i][2 * c + 1] * scale) * g[2 * c + 1]);
+    zr[lane + i * kWave] = o;
+  }
+}
+
+template <int NVL, int NT, bool kNorm, bool kAdd>
+__global__ void __launch_bounds__(kBatchThreads, NVL <= 3 ? 4 : 2)
+batched_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha,
+                      const bf16 *__restrict__ nw, float eps, bf16 *__restrict__ z,
+                      const bf16 *__restrict__ wr, int experts, int topk, int renormalize,
+                      bf16 *__restrict__ logits_out, float *__restrict__ tw,
+                      int32_t *__restrict__ tid) {
+  constexpr int kNvec = NVL * kWave, kSteps = NVL * 16, kCols = NT * 16;
+  constexpr int kWaveSteps = kSteps / kBatchWaves;
+  static_assert(kWaveSteps % kBatchSteps == 0, "k-steps per load batch");
+  __shared__ __align__(16) float part[kBatchWaves][NT][4][kWave];
+  __shared__ __align__(16) float logit[kBatchRows][kCols];
+  __shared__ __align__(16) float scratch[kBatchWaves][2 * kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int64_t row0 = (int64_t)blockIdx.x * kBatchRows;
+  if constexpr (kNorm) {
+    u32x4 gv[NVL];
+#pragma unroll
+    for (int i = 0; i < NVL; ++i) gv[i] = reinterpret_cast<const u32x4 *>(nw)[lane + i * kWave];
+    const int64_t r0 = row0 + wave * kRowsPerWave;
+    u32x4 xa[NVL], aa[NVL], xb[NVL], ab[NVL];
+    batch_load_row<NVL, kAdd>(x, a, r0, xa, aa);
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; r += 2) {
+      batch_load_row<NVL, kAdd>(x, a, r0 + r + 1, xb, ab);
+      batch_norm_row<NVL, kAdd>(x, alpha, gv, eps, z, r0 + r, xa, aa);
+      if (r + 2 < kRowsPerWave) batch_load_row<NVL, kAdd>(x, a, r0 + r + 2, xa, aa);
+      batch_norm_row<NVL, kAdd>(x, alpha, gv, eps, z, r0 + r + 1, xb, ab);
+    }
+    __syncthreads();  // every wave reads all 16 rows of z back below
+  }
+  const int tr = lane % 16, kg = lane / 16;
+  const int64_t k0 = (int64_t)wave * kWaveSteps * 4 + kg;  // 16-byte word of the wave's first k-step
+  const u32x4 *ap = reinterpret_cast<const u32x4 *>(kNorm ? z : x) + (row0 + tr) * kNvec + k0;
+  const u32x4 *bp[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+    bp[n] = reinterpret_cast<const u32x4 *>(wr) + (int64_t)min(16 * n + tr, experts - 1) * kNvec + k0;
+  f32x4 acc[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < kWaveSteps; s0 += kBatchSteps) {
+    u32x4 av[kBatchSteps], bv[kBatchSteps][NT];
+#pragma unroll
+    for (int u = 0; u < kBatchSteps; ++u) {
+      av[u] = ap[4 * (s0 + u)];
+#pragma unroll
+      for (int n = 0; n < NT; ++n) bv[u][n] = bp[n][4 * (s0 + u)];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatchSteps; ++u)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[n] = mfma16x16x32(av[u], bv[u][n], acc[n]);
+  }
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[wave][n][i][lane] = acc[n][i];
+  __syncthreads();
+  // C layout: lane l of a tile holds rows 4*(l/16) + i of column l % 16.
+  for (int idx = threadIdx.x; idx < NT * 4 * kWave; idx += kBatchThreads) {
+    const int n = idx / (4 * kWave), i = idx / kWave % 4, l = idx % kWave;
+    float sum = part[0][n][i][l];
+#pragma unroll
+    for (int w = 1; w < kBatchWaves; ++w) sum += part[w][n][i][l];
+    const int e = 16 * n + l % 16, row = 4 * (l / 16) + i;
+    const uint32_t h = f32_to_bf16(sum);
+    logit[row][e] = bf16_to_f32(h);
+    if (logits_out && e < experts) logits_out[(row0 + row) * experts + e] = (bf16)h;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = wave * kRowsPerWave; r < (wave + 1) * kRowsPerWave; ++r)
+    select_topk_lanes(logit[r], scratch[wave], lane, experts, topk, renormalize,
+                      tw + (row0 + r) * topk, tid + (row0 + r) * topk);
+}
+
+// Routes the first tokens - tokens % kBatchRows tokens with
+// batched_router_kernel when the shape allows it; returns how many it routed
+// (0: none, the per-token kernels route them all).
+template <bool kNorm, bool kAdd>
+int64_t launch_batched_router(int64_t tokens, int64_t hidden, bf16 *x, const bf16 *a,
+                              float alpha, const bf16 *nw, float eps, bf16 *z, const bf16 *wr,
+                              int experts, int topk, int renormalize, bf16 *logits_out,
+                              float *tw, int32_t *tid, hipStream_t s) {
+  const int nv = fast_nv(hidden);
+  if (tokens < kBatchRouterMinTokens || !nv || experts > kWave || experts <= 16) return 0;
+  const int64_t rows = tokens - tokens % kBatchRows;
+  const int nt = (experts + 15) / 16;
+  const dim3 grid((unsigned)(rows / kBatchRows));
+#define LM_BATCH_ROUTER(NVL, NT)                                                                \
+  if (nv == NVL && nt == NT) {                                                                  \
+    batched_router_kernel<NVL, NT, kNorm, kAdd><<<grid, kBatchThreads, 0, s>>>(                         \
+        x, a, alpha, nw, eps, z, wr, experts, topk, renormalize, logits_out, tw, tid);          \
+    return rows;                                                                                \
+  }
+#define LM_BATCH_ROUTER_NT(NVL) LM_BATCH_ROUTER(NVL, 2) LM_BATCH_ROUTER(NVL, 3) LM_BATCH_ROUTER(NVL, 4)
+  LM_BATCH_ROUTER_NT(1) LM_BATCH_ROUTER_NT(2) LM_BATCH_ROUTER_NT(3) LM_BATCH_ROUTER_NT(4)
+  LM_BATCH_ROUTER_NT(6) LM_BATCH_ROUTER_NT(8)
+#undef LM_BATCH_ROUTER_NT
+#undef LM_BATCH_ROUTER
+  return 0;
+}
+
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / kWave;
 constexpr int kMaxAlignExperts = 511;
@@ -691,10 +891,16 @@ extern "C" int lm_router(const void *x, const void *gate_weight, int64_t tokens,
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(x && gate_weight && topk_weights && topk_ids);
   if (const int nv = fast_nv(hidden)) {
-    launch_fast_router<false, false>(nv, tokens, (bf16 *)x, nullptr, 0.f, nullptr, 0.f, nullptr,
-                                     (const bf16 *)gate_weight, (int)experts, (int)topk,
-                                     renormalize, (bf16 *)logits_out, topk_weights, topk_ids,
-                                     (hipStream_t)stream);
+    const int64_t done = launch_batched_router<false, false>(
+        tokens, hidden, (bf16 *)x, nullptr, 0.f, nullptr, 0.f, nullptr, (const bf16 *)gate_weight,
+        (int)experts, (int)topk, renormalize, (bf16 *)logits_out, topk_weights, topk_ids,
+        (hipStream_t)stream);
+    if (done < tokens)
+      launch_fast_router<false, false>(
+          nv, tokens - done, (bf16 *)x + done * hidden, nullptr, 0.f, nullptr, 0.f, nullptr,
+          (const bf16 *)gate_weight, (int)experts, (int)topk, renormalize,
+          logits_out ? (bf16 *)logits_out + done * experts : nullptr, topk_weights + done * topk,
+          topk_ids + done * topk, (hipStream_t)stream);
     LM_CHECK_LAUNCH();
     return LM_OK;
   }
@@ -717,18 +923,35 @@ extern "C" int lm_add_rmsnorm_router(void *x, const void *a, float alpha, const 
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(x && norm_weight && z && gate_weight && topk_weights && topk_ids);
   if (const int nv = fast_nv(hidden)) {
-    if (a)
-      launch_fast_router<true, true>(nv, tokens, (bf16 *)x, (const bf16 *)a, alpha,
-                                     (const bf16 *)norm_weight, eps, (bf16 *)z,
-                                     (const bf16 *)gate_weight, (int)experts, (int)topk,
-                                     renormalize, (bf16 *)logits_out, topk_weights, topk_ids,
-                                     (hipStream_t)stream);
-    else
-      launch_fast_router<true, false>(nv, tokens, (bf16 *)x, nullptr, 0.f,
-                                      (const bf16 *)norm_weight, eps, (bf16 *)z,
-                                      (const bf16 *)gate_weight, (int)experts, (int)topk,
-                                      renormalize, (bf16 *)logits_out, topk_weights, topk_ids,
-                                      (hipStream_t)stream);
+    const hipStream_t s = (hipStream_t)stream;
+    const int64_t done =
+        a ? launch_batched_router<true, true>(tokens, hidden, (bf16 *)x, (const bf16 *)a, alpha,
+                                              (const bf16 *)norm_weight, eps, (bf16 *)z,
+                                              (const bf16 *)gate_weight, (int)experts, (int)topk,
+                                              renormalize, (bf16 *)logits_out, topk_weights,
+                                              topk_ids, s)
+          : launch_batched_router<true, false>(tokens, hidden, (bf16 *)x, nullptr, 0.f,
+                                               (const bf16 *)norm_weight, eps, (bf16 *)z,
+                                               (const bf16 *)gate_weight, (int)experts,
+                                               (int)topk, renormalize, (bf16 *)logits_out,
+                                               topk_weights, topk_ids, s);
+    if (done < tokens) {
+      // The per-token kernels take the rows the batched kernel left.
+      bf16 *xt = (bf16 *)x + done * hidden, *zt = (bf16 *)z + done * hidden;
+      bf16 *lt = logits_out ? (bf16 *)logits_out + done * experts : nullptr;
+      if (a)
+        launch_fast_router<true, true>(nv, tokens - done, xt, (const bf16 *)a + done * hidden,
+                                       alpha, (const bf16 *)norm_weight, eps, zt,
+                                       (const bf16 *)gate_weight, (int)experts, (int)topk,
+                                       renormalize, lt, topk_weights + done * topk,
+                                       topk_ids + done * topk, s);
+      else
+        launch_fast_router<true, false>(nv, tokens - done, xt, nullptr, 0.f,
+                                        (const bf16 *)norm_weight, eps, zt,
+                                        (const bf16 *)gate_weight, (int)experts, (int)topk,
+                                        renormalize, lt, topk_weights + done * topk,
+                                        topk_ids + done * topk, s);
+    }
     LM_CHECK_LAUNCH();
     return LM_OK;
   }

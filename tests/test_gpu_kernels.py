@@ -491,3 +491,63 @@ def test_add_rmsnorm_route_equals_unfused(with_residual, h):
     w2_, i2 = router.route(z2, wr, k, logits_out=logits2)
     assert torch.equal(x1, x2) and torch.equal(z1, z2) and torch.equal(logits1, logits2)
     assert torch.equal(i1, i2) and torch.equal(w1_, w2_)
+
+
+def per_token_logits(z, wr, k, chunk=256):
+    """Router logits from the per-token GEMV kernels (calls below the batched
+    kernel's token count)."""
+    out = torch.empty(z.shape[0], wr.shape[0], device=DEV, dtype=torch.bfloat16)
+    for c in range(0, z.shape[0], chunk):
+        router.route(z[c:c + chunk], wr, k, logits_out=out[c:c + chunk])
+    return out
+
+
+@pytest.mark.parametrize("m,h,e,k,with_residual", [(4103, 1536, 40, 8, True), (4096, 1536, 40, 8, False),
+                                                   (4111, 1024, 32, 4, True), (4100, 4096, 64, 8, True),
+                                                   (4096, 3072, 60, 6, True), (4104, 512, 20, 2, True),
+                                                   (4097, 2048, 48, 8, True)])
+@torch.inference_mode()
+def test_batched_add_rmsnorm_route(m, h, e, k, with_residual):
+    """Prefill-sized calls take the batched MFMA router (16 tokens per wave,
+    a tail below 16 on the per-token kernel): x and z bitwise the unfused
+    norm's, logits within one bf16 ulp of the GEMV kernels' and of the CPU
+    product, ids exact given the kernel's own logits."""
+    g = torch.Generator().manual_seed(m + h)
+    x = torch.randn(m, h, generator=g).to(torch.bfloat16).to(DEV)
+    a = torch.randn(m, h, generator=g).to(torch.bfloat16).to(DEV) if with_residual else None
+    w = (1 + 0.2 * torch.randn(h, generator=g)).to(torch.bfloat16).to(DEV)
+    wr = (0.02 * torch.randn(e, h, generator=g)).to(torch.bfloat16).to(DEV)
+    x1, x2 = x.clone(), x.clone()
+    logits1 = torch.empty(m, e, device=DEV, dtype=torch.bfloat16)
+    w1_, i1, z1 = router.add_rmsnorm_route(x1, a, 0.22, w, 1e-6, wr, k, logits_out=logits1)
+    z2 = norm.add_rmsnorm(x2, a, 0.22, w, 1e-6)
+    assert torch.equal(x1, x2) and torch.equal(z1, z2)
+    logits2 = per_token_logits(z2, wr, k)
+    tail = m % 16
+    if tail:
+        assert torch.equal(logits1[m - tail:], logits2[m - tail:])
+    assert within_ulp_or_abs(logits1, logits2, 1, 2e-3)
+    assert (logits1 != logits2).float().mean() < 0.02
+    cpu_logits = torch.nn.functional.linear(z1.cpu(), wr.cpu())
+    assert within_ulp_or_abs(logits1.cpu(), cpu_logits, 1, 2e-3)
+    ew, eids = ops.route(logits1.cpu(), k)
+    assert torch.equal(i1.cpu(), eids)
+    torch.testing.assert_close(w1_.cpu(), ew, rtol=2e-6, atol=1e-7)
+    # without logits_out the same selection
+    x3 = x.clone()
+    w3_, i3, z3 = router.add_rmsnorm_route(x3, a, 0.22, w, 1e-6, wr, k)
+    assert torch.equal(i3, i1) and torch.equal(w3_, w1_) and torch.equal(z3, z1)
+
+
+@pytest.mark.parametrize("renormalize", [True, False])
+@torch.inference_mode()
+def test_batched_route_without_norm(renormalize):
+    m, h, e, k = 4099, 1536, 40, 8
+    z = bf((m, h), 1.0, 77).to(DEV)
+    wr = bf((e, h), 0.02, 78).to(DEV)
+    logits = torch.empty(m, e, device=DEV, dtype=torch.bfloat16)
+    weights, ids = router.route(z, wr, k, renormalize=renormalize, logits_out=logits)
+    assert within_ulp_or_abs(logits, per_token_logits(z, wr, k), 1, 2e-3)
+    ew, eids = ops.route(logits.cpu(), k, renormalize=renormalize)
+    assert torch.equal(ids.cpu(), eids)
+    torch.testing.assert_close(weights.cpu(), ew, rtol=2e-6, atol=1e-7)

@@ -167,3 +167,32 @@ def test_add_rmsnorm_route_splitk_limits():
         router.add_rmsnorm_route_splitk(x3, torch.zeros(2, 4, 3072, device=DEV), 0.2,
                                         torch.ones(3072, dtype=torch.bfloat16, device=DEV), 1e-6,
                                         torch.zeros(40, 3072, dtype=torch.bfloat16, device=DEV), 8)
+
+
+@torch.inference_mode()
+def test_bf16_rounding_of_every_float():
+    """Every kernel rounds fp32 to bf16 with one helper (the hardware
+    conversion plus NaN canonicalisation). The split-K reduce with one slice
+    writes bf16(0 + p), i.e. that rounding of p (p = -0 gives +0), so all
+    2^32 bit patterns go through it: against round-to-nearest-even with NaN ->
+    0x7fc0 computed in integers, and against torch's CPU conversion on a
+    sample of every chunk (non-NaN inputs: torch's own NaN patterns differ
+    between its scalar conversion, 0x7fc0, and its vectorised one, 0xffff)."""
+    rows, n = 1 << 16, 1 << 12
+    chunk = rows * n
+    for base in range(0, 1 << 32, chunk):
+        u = torch.arange(base, base + chunk, device=DEV, dtype=torch.int64)
+        p = u.to(torch.int32).view(torch.float32)
+        out = linear.reduce(p.view(1, rows, n)).view(-1).view(torch.int16).to(torch.int64) & 0xFFFF
+        rne = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+        exp = torch.where(torch.isnan(p), torch.full_like(u, 0x7FC0), rne & 0xFFFF)
+        exp = torch.where(u == 0x80000000, torch.zeros_like(exp), exp)
+        assert torch.equal(out, exp), hex(base)
+        idx = torch.randint(0, chunk, (1 << 16,), device=DEV)
+        sample = p[idx].cpu()
+        got = out[idx].cpu()
+        ref = sample.to(torch.bfloat16).view(torch.int16).to(torch.int64) & 0xFFFF
+        ref = torch.where(sample.view(torch.int32) == -0x80000000, torch.zeros_like(ref), ref)
+        nan = torch.isnan(sample)
+        assert torch.equal(got[~nan], ref[~nan]), hex(base)
+        assert bool((got[nan] == 0x7FC0).all()), hex(base)
