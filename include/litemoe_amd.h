@@ -179,7 +179,12 @@ int lm_prefill_attention(const void *q, int64_t qs0, int64_t qs1,
  * (model.py:115-116). x: [tokens, hidden] bf16, Wr: [experts, hidden] bf16,
  * hidden % 8 == 0, hidden <= 4096, experts <= 256, topk <= min(experts, 16).
  * Ties among the selected are ordered by id; the weights' denominator is
- * summed in selection order. */
+ * summed in selection order. The fp32 accumulation order of the logits
+ * depends on the call size: below 1024 tokens a per-token GEMV; from 1024
+ * tokens with hidden = 512*{1,2,3,4,6,8} and 16 < experts <= 64, MFMA tiles
+ * of 16 tokens (the last tokens % 16 on the GEMV), so a logit can differ by
+ * one bf16 ulp between the two, as between any two BLAS orders. The
+ * selection is exact given the logits. */
 int lm_router(const void *x, const void *gate_weight, int64_t tokens,
               int64_t hidden, int64_t experts, int64_t topk, int renormalize,
               void *logits_out, float *topk_weights, int32_t *topk_ids,
@@ -304,7 +309,8 @@ int lm_linear_splitk_reduce(const float *partials, int64_t splits, int64_t rows,
  *   then lm_router on z[t] (logits_out may be NULL).
  * a may be NULL (x only normalised). Fuses litemoe/model.py:108-113: the
  * residual update, the post-attention norm, the router GEMV and vLLM
- * fused_topk. Same limits as lm_router. */
+ * fused_topk. Same limits and logit accumulation orders as lm_router; x and
+ * z are bitwise those of lm_add_rmsnorm at every size. */
 int lm_add_rmsnorm_router(void *x, const void *a, float alpha,
                           const void *norm_weight, float eps, void *z,
                           const void *gate_weight, int64_t tokens,
