@@ -456,6 +456,29 @@ def test_moe_routes_scan_path_equals_block_path(m):
         assert rel_l2(scan.cpu(), ops.expert_routes(x, ids, w1, w2)) < 1e-2
 
 
+@pytest.mark.parametrize("m,e,hot", [(64, 40, False), (64, 40, True), (60, 36, False), (64, 33, True),
+                                     (48, 40, True), (64, 40, None)])
+@torch.inference_mode()
+def test_gate_up_scan_path_equals_block_path(m, e, hot):
+    """The decode gate/up (each expert's workgroups collect its routes from
+    topk_ids) equals the aligned-block path bit for bit, including experts
+    with more than 16 routes (hot: four experts in every token's top-8, up to
+    64 routes each) and experts with none (None: only 8 experts used)."""
+    h, i, k = 1536, 512, 8
+    x, w1, _, _, ids = _moe_inputs(m, h, i, e, k, 500 + m + e)
+    g = torch.Generator().manual_seed(m + e)
+    if hot:  # distinct ids per token: 0..3, then four of 4..e-1
+        ids = torch.stack([torch.cat([torch.arange(4), 4 + torch.randperm(e - 4, generator=g)[:4]])
+                           for _ in range(m)]).int()
+    elif hot is None:
+        ids = torch.stack([torch.randperm(8, generator=g) for _ in range(m)]).int()
+    xd, w1d, idsd = x.to(DEV), w1.to(DEV), ids.to(DEV)
+    scan = experts.gate_up(xd, w1d, None, None, k, topk_ids=idsd)
+    offsets, order, _ = experts.moe_align(idsd, e)
+    blocks = experts.gate_up(xd, w1d, offsets, order, k, block_rows=16)
+    assert torch.equal(scan, blocks)
+
+
 @torch.inference_mode()
 def test_finish_add_rmsnorm_equals_unfused():
     m, h, k, e = 64, 1536, 8, 40
