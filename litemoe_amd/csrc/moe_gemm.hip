@@ -367,6 +367,71 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
   }
 }
 
+// The decode scan path of the down projection as a kernel of its own, as
+// gate_up_scan_kernel is for gate/up: weights prefetched before the scan,
+// activation rows past the route set repeating its last route (no
+// divergent loads), no row-block loop for sets of at most 16 routes. A
+// workgroup covers NT MFMA tiles of 16 output columns (KS: 32-wide k steps
+// per wave, inter = KS * 32 * kWaves). Same MFMA order and wave-order sum as
+// down_kernel, hence the same bits.
+template <int KS, int NT>
+__global__ void __launch_bounds__(kThreads)
+down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
+                 const int32_t *__restrict__ ids, int routes, int hidden, int inter,
+                 bf16 *__restrict__ y) {
+  __shared__ float red[kWaves][NT][4][kWave];
+  __shared__ int list[kMaxScanRows];
+  __shared__ int wave_count[kWaves];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int col = lane % 16, grp = lane / 16;
+  const int e = blockIdx.y, n0 = blockIdx.x * 16 * NT;
+  const int kbase = wave * KS * 32 + grp * 8;
+  const bf16 *w0 = w2 + ((int64_t)e * hidden + n0 + col) * inter + kbase;
+  u32x4 b[NT][KS], a[KS];
+  const ScanIds scan = load_ids(ids, routes);
+  __builtin_amdgcn_sched_barrier(0);  // ids first: the scan waits for them only
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int s = 0; s < KS; ++s) b[t][s] = load16(w0 + (int64_t)t * 16 * inter + s * 32);
+  __builtin_amdgcn_sched_barrier(0);
+  const int n = scan_ids(scan, e, list, wave_count);
+  if (n == 0) return;
+  auto block = [&](int rb) {
+    const bf16 *ar = act + (int64_t)list[min(rb + col, n - 1)] * inter + kbase;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) a[s] = load16(ar + s * 32);
+    f32x4 c[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) c[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) c[t] = mfma16x16x32(a[s], b[t][s], c[t]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][t][i][lane] = c[t][i];
+    __syncthreads();
+    // Wave w finishes C row 4*grp + w of every lane group.
+    const int row = rb + grp * 4 + wave;
+    bf16 *yr = y + (int64_t)list[min(row, n - 1)] * hidden + n0 + col;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) v += red[w][t][wave][lane];
+      if (row < n) yr[16 * t] = (bf16)f32_to_bf16(v);
+    }
+    __syncthreads();
+  };
+  if (n <= 16) {
+    block(0);
+  } else {
+    for (int rb = 0; rb < n; rb += 16) block(rb);
+  }
+}
+
 // Supported k steps per wave (reduction length / 128).
 #define LM_KS_LIST(X) X(1) X(2) X(3) X(4) X(6) X(8) X(12) X(16)
 
@@ -446,6 +511,25 @@ int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const i
   if (gy > 65535) return LM_EUNSUPPORTED;
   const dim3 grid((unsigned)(hidden / 32), (unsigned)gy);
   const int mode = route_mode(scan, routes, experts);
+#ifndef LM_DOWN_SCAN_TILES
+#define LM_DOWN_SCAN_TILES 4
+#endif
+  constexpr int kNT = LM_DOWN_SCAN_TILES;
+  if (kNT > 0 && mode == kScanPrefetch && hidden % (16 * kNT) == 0 && inter <= 8 * 128) {
+    const dim3 sgrid((unsigned)(hidden / (16 * kNT)), (unsigned)experts);
+    switch (inter / 128) {
+#define X(KS)                                                                                  \
+  case KS:                                                                                     \
+    down_scan_kernel<KS, (kNT > 0 ? kNT : 1)><<<sgrid, kThreads, 0, stream>>>(                 \
+        act, w2, ids, (int)routes, (int)hidden, (int)inter, y);                                \
+    LM_CHECK_LAUNCH();                                                                         \
+    return LM_OK;
+      X(1) X(2) X(3) X(4) X(6) X(8)
+#undef X
+      default:
+        break;
+    }
+  }
   switch (inter / 128) {
 #define X(KS)                                                                                  \
   case KS:                                                                                     \
