@@ -372,8 +372,9 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
 // activation rows past the route set repeating its last route (no
 // divergent loads), no row-block loop for sets of at most 16 routes. A
 // workgroup covers NT MFMA tiles of 16 output columns (KS: 32-wide k steps
-// per wave, inter = KS * 32 * kWaves). Same MFMA order and wave-order sum as
-// down_kernel, hence the same bits.
+// per wave, inter = KS * 32 * kWaves); its activation loads are issued back
+// to back. Same MFMA order and wave-order sum as down_kernel, hence the same
+// bits.
 template <int KS, int NT>
 __global__ void __launch_bounds__(kThreads)
 down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
@@ -401,6 +402,7 @@ down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
     const bf16 *ar = act + (int64_t)list[min(rb + col, n - 1)] * inter + kbase;
 #pragma unroll
     for (int s = 0; s < KS; ++s) a[s] = load16(ar + s * 32);
+    __builtin_amdgcn_sched_barrier(0);  // all activation loads in flight before the MFMAs
     f32x4 c[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) c[t] = f32x4{0.f, 0.f, 0.f, 0.f};
