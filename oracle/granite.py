@@ -68,9 +68,10 @@ class Granite:
         return F.linear(z, self.w["head"]) / cfg.logits_scaling
 
     # -- prefill of one sequence into cache row ``slot`` -----------------------
-    def prefill(self, prompt, cache, slot):
-        """All-position logits ``[T, V]`` of one prompt; K/V of positions
-        0..T-1 go to cache row ``slot`` (cache.py:28-38 / packed.py)."""
+    def prefill(self, prompt, cache, slot, last_only=False):
+        """All-position logits ``[T, V]`` of one prompt (``[1, V]`` for the
+        last position with ``last_only``); K/V of positions 0..T-1 go to cache
+        row ``slot`` (cache.py:28-38 / packed.py)."""
         cfg = self.cfg
         tokens = torch.tensor(prompt)
         t = tokens.numel()
@@ -88,7 +89,7 @@ class Granite:
             x = self._residual(x, F.linear(a, w["self_attn.o_proj"]))
             z = ops.rmsnorm(x, w["post_attention_layernorm"], cfg.rms_norm_eps)
             x = self._residual(x, self._moe(z, w, valid, False))
-        return self._logits(x)
+        return self._logits(x[-1:] if last_only else x)
 
     # -- one decode step -------------------------------------------------------
     def decode(self, tokens, positions, valid, cache):

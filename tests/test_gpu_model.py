@@ -68,6 +68,50 @@ def test_prefill_and_decode_logits_match_oracle(lean):
     assert agree >= steps - 1
 
 
+@pytest.mark.parametrize("name", ["granite-1b", "granite-3b"])
+@torch.inference_mode()
+def test_benchmark_shapes_prefill_and_decode_match_oracle(name):
+    """cfg 2 / cfg 3 per-layer shapes (hidden 1024 / 1536, 16/8 and 24/8
+    heads, 32 / 40 experts top-8, intermediate 512, vocab 49155) with two
+    layers of random bf16 weights: packed prefill of four ragged prompts,
+    then lean decode steps (split-K projections, fused attention, fused
+    router, scan-path experts, greedy epilogue shapes) against the oracle's
+    production rounding. Logits within rel-L2 2e-2 per step, greedy argmax
+    agreement."""
+    from litemoe_amd import synth
+    from litemoe_amd.config import preset
+    cfg = preset(name, num_hidden_layers=2)
+    w_gpu = synth.granite_weights(cfg, seed=4, device=DEV, method="torch")
+    w_cpu = {k: ([{n: t.cpu() for n, t in layer.items()} for layer in v] if k == "layers" else v.cpu())
+             for k, v in w_gpu.items()}
+    ep = ExpertParallel(1, 0, 4096, cfg.hidden_size, cfg.num_experts_per_tok, torch.bfloat16, DEV,
+                        HipFusedExperts())
+    cap = 64
+    model, ref = Granite(cfg, w_gpu, ep, cap), oracle.Granite(cfg, w_cpu, cap, fused=True)
+    prompts = synth.prompts(4, [23, 9, 40, 17], cfg.vocab_size, 6)
+    cache = KVCache(cfg, len(prompts), cap, DEV, torch.bfloat16)
+    rcache = oracle.Cache(cfg, len(prompts), cap, torch.bfloat16)
+    logits = packed_prefill_logits(model, prompts, cache)[:, 0].cpu()
+    expected = torch.cat([ref.prefill(p, rcache, j, last_only=True) for j, p in enumerate(prompts)])
+    assert rel_l2(logits, expected) < 2e-2
+    assert int((logits.argmax(-1) == expected.argmax(-1)).sum()) >= 3
+    tokens = expected.argmax(-1)
+    lengths = torch.tensor([len(p) for p in prompts])
+    model.decode_lean = model.ep.decode_lean = True
+    agree, steps = 0, 0
+    for step in range(4):
+        valid = torch.ones(len(prompts), dtype=torch.bool)
+        got = model.forward(tokens[:, None].to(DEV), lengths[:, None].to(DEV), valid[:, None].to(DEV),
+                            cache)[:, 0].cpu()
+        exp = ref.decode(tokens, lengths, valid, rcache)
+        assert rel_l2(got, exp) < 2e-2, step
+        agree += int((got.argmax(-1) == exp.argmax(-1)).sum())
+        steps += len(prompts)
+        tokens = exp.argmax(-1)
+        lengths += 1
+    assert agree >= steps - 1
+
+
 @torch.inference_mode()
 def test_engine_modes_identical_and_close_to_oracle_greedy():
     """Reference test_cuda_execution.py:102-133: graph and graph-async equal
