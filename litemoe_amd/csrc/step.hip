@@ -88,7 +88,7 @@ prologue_kernel(const uint8_t *__restrict__ active, const int64_t *__restrict__ 
 }
 
 constexpr int kArgThreads = 1024;
-constexpr int kArgBatch = 16;
+constexpr int kArgChunks = 8;  // 16-byte loads per lane in flight
 
 // (value, index) order of torch.argmax: larger value first, then lower index;
 // NaN above everything (torch.argmax returns the first NaN).
@@ -109,22 +109,35 @@ epilogue_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, 
   __shared__ float sv[kArgThreads / kWave];
   __shared__ int si[kArgThreads / kWave];
   const int64_t row = blockIdx.x;
-  const bf16 *lr = logits + row * ld;
+  // The row is read in aligned 16-byte chunks (rows of an odd vocab start
+  // anywhere): chunk c holds values 8c - lead .. 8c - lead + 7, and only
+  // those in [0, vocab) count. An aligned chunk never leaves the page of the
+  // row value it holds.
+  const uintptr_t start = reinterpret_cast<uintptr_t>(logits + row * ld);
+  const u32x4 *chunks = reinterpret_cast<const u32x4 *>(start & ~(uintptr_t)15);
+  const int lead = (int)((start & 15) / 2);
+  const int nchunks = (lead + vocab + 7) / 8;
   float best = -INFINITY;
   int bi = vocab;  // none yet
-  // kArgBatch loads in flight per lane before any compare (indices clamped,
-  // then masked), so a row costs a few memory latencies, not one per value.
-  for (int base = threadIdx.x; base < vocab; base += kArgThreads * kArgBatch) {
-    uint32_t raw[kArgBatch];
+  // kArgChunks loads in flight per lane before any compare (chunk indices
+  // clamped, values masked), so a row costs one memory latency per round.
+  for (int base = threadIdx.x; base < nchunks; base += kArgThreads * kArgChunks) {
+    u32x4 raw[kArgChunks];
 #pragma unroll
-    for (int u = 0; u < kArgBatch; ++u) raw[u] = lr[min(base + u * kArgThreads, vocab - 1)];
+    for (int u = 0; u < kArgChunks; ++u) raw[u] = chunks[min(base + u * kArgThreads, nchunks - 1)];
 #pragma unroll
-    for (int u = 0; u < kArgBatch; ++u) {
-      const int v = base + u * kArgThreads;
-      const float s = round_bf16(bf16_to_f32(raw[u]) * inv_scaling);
-      if (v < vocab && better(s, v, best, bi)) {
-        best = s;
-        bi = v;
+    for (int u = 0; u < kArgChunks; ++u) {
+      float f[8];
+      unpack8(raw[u], f);
+      const int v0 = (base + u * kArgThreads) * 8 - lead;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int v = v0 + j;
+        const float sc = round_bf16(f[j] * inv_scaling);
+        if (base + u * kArgThreads < nchunks && v >= 0 && v < vocab && better(sc, v, best, bi)) {
+          best = sc;
+          bi = v;
+        }
       }
     }
   }
