@@ -113,18 +113,22 @@ epilogue_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, 
   // anywhere): chunk c holds values 8c - lead .. 8c - lead + 7, and only
   // those in [0, vocab) count. An aligned chunk never leaves the page of the
   // row value it holds.
-  const uintptr_t start = reinterpret_cast<uintptr_t>(logits + row * ld);
-  const u32x4 *chunks = reinterpret_cast<const u32x4 *>(start & ~(uintptr_t)15);
-  const int lead = (int)((start & 15) / 2);
+  const bf16 *lr = logits + row * ld;
+  const int mis = (int)(reinterpret_cast<uintptr_t>(lr) & 15);  // bytes past the last 16-byte boundary
+  const u32x4 *chunks = reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(lr) - mis);
+  const int lead = mis / 2;
   const int nchunks = (lead + vocab + 7) / 8;
-  float best = -INFINITY;
-  int bi = vocab;  // none yet
-  // kArgChunks loads in flight per lane before any compare (chunk indices
-  // clamped, values masked), so a row costs one memory latency per round.
-  for (int base = threadIdx.x; base < nchunks; base += kArgThreads * kArgChunks) {
-    u32x4 raw[kArgChunks];
+  // A lane visits its values in increasing index order, so a strict
+  // comparison of orderable keys (NaN above everything) keeps the first
+  // index of its maximum; lanes and waves then merge with better().
+  uint32_t bk = 0;  // below every real key
+  int bi = vocab;   // none yet
+  u32x4 raw[kArgChunks];
+  auto load = [&](int base) {
 #pragma unroll
     for (int u = 0; u < kArgChunks; ++u) raw[u] = chunks[min(base + u * kArgThreads, nchunks - 1)];
+  };
+  auto scan = [&](int base) {
 #pragma unroll
     for (int u = 0; u < kArgChunks; ++u) {
       float f[8];
@@ -133,13 +137,37 @@ epilogue_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, 
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int v = v0 + j;
-        const float sc = round_bf16(f[j] * inv_scaling);
-        if (base + u * kArgThreads < nchunks && v >= 0 && v < vocab && better(sc, v, best, bi)) {
-          best = sc;
+        uint32_t h = f32_to_bf16(f[j] * inv_scaling);
+        h = h == 0x8000u ? 0u : h;  // -0 ties with +0, as in a float compare
+        const uint32_t key = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);  // NaN is 0x7fc0: top
+        const bool in = base + u * kArgThreads < nchunks && v >= 0 && v < vocab;
+        if (in && key + 1u > bk) {  // key + 1 > 0 for every real value
+          bk = key + 1u;
           bi = v;
         }
       }
     }
+  };
+  // First round (rows up to 8 * kArgThreads * kArgChunks values): every
+  // chunk load, then the row's state, are issued before anything waits; the
+  // state is used only at the end. eos may be NULL when neos == 0: the row's
+  // own counter is read instead.
+  load(threadIdx.x);
+  const bool val = valid[row] != 0;
+  const int64_t gen = generated[row], len = length[row], bud = budget[row];
+  const int64_t eos_read = *(neos > 0 ? eos : generated + row);
+  __builtin_amdgcn_sched_barrier(0);
+  scan(threadIdx.x);
+  for (int base = threadIdx.x + kArgThreads * kArgChunks; base < nchunks;
+       base += kArgThreads * kArgChunks) {
+    load(base);
+    scan(base);
+  }
+  const int64_t eos_first = neos > 0 ? eos_read : -1;
+  float best = -INFINITY;
+  if (bi < vocab) {
+    const uint32_t key = bk - 1u;
+    best = bf16_to_f32((key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu));
   }
   // Wave then workgroup reduction of (value, index).
 #pragma unroll
@@ -164,18 +192,18 @@ epilogue_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, 
         bi = si[w];
       }
     const int64_t candidate = bi;
-    const bool val = valid[row] != 0;
-    const int64_t gen = generated[row];
     emit[row * 3 + 0] = candidate;
     emit[row * 3 + 1] = gen;
     emit[row * 3 + 2] = val;
     const int64_t gen1 = gen + (val ? 1 : 0);
-    length[row] += val ? 1 : 0;
+    length[row] = len + (val ? 1 : 0);
     generated[row] = gen1;
     if (val) next[row] = candidate;
-    bool done = gen1 >= budget[row];
-    if (!ignore_eos)
-      for (int e = 0; e < neos; ++e) done = done || candidate == eos[e];
+    bool done = gen1 >= bud;
+    if (!ignore_eos && neos > 0) {
+      done = done || candidate == eos_first;
+      for (int e = 1; e < neos; ++e) done = done || candidate == eos[e];
+    }
     active[row] = val && !done;
   }
 }

@@ -116,6 +116,31 @@ def test_epilogue_equals_reference_step(rows, vocab, scaling, ignore_eos):
 
 
 @torch.inference_mode()
+def test_epilogue_signed_zeros_infinities_and_negative_rows():
+    """torch.argmax semantics on the edge values: -0 ties with +0 (first
+    index wins), -inf rows, all-negative rows, NaN after a maximum, +inf."""
+    vocab = 1003
+    raw = torch.full((6, vocab), -3.0, dtype=torch.bfloat16)
+    raw[0, 10], raw[0, 5] = 0.0, -0.0            # max 0: index 5 (-0) comes first
+    raw[1, 7], raw[1, 900] = -0.0, 0.0           # max 0: index 7
+    raw[2] = -float("inf")                       # all -inf: index 0
+    raw[3] = -torch.arange(vocab, dtype=torch.float32).to(torch.bfloat16) - 1  # all negative: index 0
+    raw[4, 400], raw[4, 401] = float("inf"), float("nan")  # NaN beats +inf
+    raw[5, 999], raw[5, 2] = 5.0, 5.0            # tie: index 2
+    raw = raw.to(DEV)
+    s = state_for(6, vocab, 3)
+    valid = torch.ones(6, dtype=torch.bool, device=DEV)
+    eos = torch.zeros(0, dtype=torch.int64, device=DEV)
+    exp_s = {k: v.clone() for k, v in s.items()}
+    exp_emit = torch.zeros(6, 3, dtype=torch.int64, device=DEV)
+    got_emit = exp_emit.clone()
+    reference_step(raw, 6.0, valid, exp_s, exp_emit, eos, True)
+    step.greedy_epilogue(raw, 6.0, valid, s, got_emit, eos, True)
+    assert torch.equal(got_emit, exp_emit)
+    assert got_emit[:, 0].tolist() == [5, 7, 0, 0, 401, 2]
+
+
+@torch.inference_mode()
 def test_epilogue_strided_logits():
     raw = normal_bf16((4, 3000), 2.0, 5).to(DEV)
     view = raw[:, :2999]  # row stride 3000
