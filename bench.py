@@ -30,7 +30,9 @@ line (not the driver's decode line):
                   the same token counts;
   --flash-decode  cfg 5: decode attention over B=128 rows with contexts
                   U{1024..4096} (seed 3), capacity 4096, KV filled N(0,1):
-                  GB/s of the KV stream against 8 TB/s.
+                  GB/s of the KV stream against 8 TB/s;
+  --long-decode   cfg 5: the whole hipGraph decode step at B=128 with
+                  prompts U{1024..4032} (seed 3), capacity 4096: step tok/s.
 """
 import argparse
 import json
@@ -69,6 +71,7 @@ def parse():
                     help="only copy a 256 MiB device buffer 3 times (FETCH/WRITE counter calibration)")
     ap.add_argument("--prefill", action="store_true", help="cfg 4 packed prefill (own JSON line)")
     ap.add_argument("--flash-decode", action="store_true", help="cfg 5 decode attention (own JSON line)")
+    ap.add_argument("--long-decode", action="store_true", help="cfg 5 decode step tok/s (own JSON line)")
     return ap.parse_args()
 
 
@@ -257,6 +260,63 @@ def flash_decode_bench(args):
     print(json.dumps(line), flush=True)
 
 
+def long_decode_bench(args):
+    """cfg 5: decode steps at B=128 over ragged long contexts (one JSON line)."""
+    import torch
+
+    from litemoe_amd import synth
+    from litemoe_amd.config import preset
+    from litemoe_amd.engine import Request
+    from litemoe_amd.ep import ExpertParallel
+    from litemoe_amd.experts import HipFusedExperts
+    from litemoe_amd.model import Granite
+    from litemoe_amd.optimized import OptimizedEngine
+
+    dev = torch.device("cuda:0")
+    cfg = preset(args.model)
+    batch, cap, steps, warmup = 128, 4096, 32, 5
+    lengths = synth.ragged_lengths(batch, 1024, cap - 64, 3)
+    w = synth.granite_weights(cfg, seed=0, device=dev, method="torch")
+    ep = ExpertParallel(1, 0, batch, cfg.hidden_size, cfg.num_experts_per_tok, torch.bfloat16, dev,
+                        HipFusedExperts())
+    model = Granite(cfg, w, ep, cap)
+    prompts = synth.prompts(batch, lengths, cfg.vocab_size, 1)
+    requests = [Request(str(i), p, 48) for i, p in enumerate(prompts)]
+    engine = OptimizedEngine(model, requests, mode="graph", ignore_eos=True, capacity=cap)
+    with torch.inference_mode():
+        engine.prepare_graph()
+        engine.reset()
+        t = time.perf_counter()
+        engine.prefill()
+        torch.cuda.synchronize()
+        log(f"prefill of {sum(lengths)} tokens ({batch} prompts) in {time.perf_counter() - t:.2f}s")
+        snapshot = {k: v.clone() for k, v in engine.state.items()}
+        for _ in range(warmup):
+            engine.graph.replay()
+        torch.cuda.synchronize()
+        for k, v in snapshot.items():
+            engine.state[k].copy_(v)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            engine.graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        assert bool(engine.state["active"].all())
+    kv = sum(n + steps // 2 for n in lengths) * cfg.num_key_value_heads * 64 * 2 * 2 * cfg.num_hidden_layers
+    line = {
+        "metric": "decode tok/s, cfg5 (B=128, contexts U{1024..4032})", "value": round(batch * steps / elapsed, 1),
+        "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(elapsed * 1e3 / steps, 4),
+        "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights (seed 0), prompt ids (seed 1), lengths seed 3",
+        "config": {"workload": "cfg5 decode: granite-3b shape, batch 128, ragged prompts U{1024..4032}, capacity 4096, "
+                               "one hipGraph per decode step", "batch": batch, "capacity": cap,
+                   "mean_context": round(sum(lengths) / batch + steps / 2, 1)},
+        "kv_bytes_per_step": kv,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def cpu_baseline(model, cfg, engine, state, layers, batch):
     """Time the CPU oracle's decode step on ``layers`` of the model's layers
     (weights and filled KV cache copied from the GPU), extrapolate to all."""
@@ -319,6 +379,8 @@ def main():
         return prefill_bench(args)
     if args.flash_decode:
         return flash_decode_bench(args)
+    if args.long_decode:
+        return long_decode_bench(args)
 
     from litemoe_amd import synth
     from litemoe_amd.config import preset
@@ -394,20 +456,25 @@ def main():
 
     gate_gbs = roof["gate_up_bytes"] / (roof["gate_up_us"] * 1e-6) / 1e9
     fused_gbs = roof["fused_bytes"] / (roof["fused_us"] * 1e-6) / 1e9
+    headline = args.model == "granite-3b" and args.batch == 64  # the profiled configuration
+    name = {"granite-3b": "cfg3", "granite-1b": "cfg2"}.get(args.model, args.model)
     line = {
-        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC if headline else f"decode tok/s, {args.model} shape bf16 bs={args.batch}",
+        "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: random-init bf16 weights N(0,0.02) (torch generator, seed 0), random prompt ids (seed 1)",
-        "config": {"workload": (f"cfg3 decode: {args.model} shape (32 layers, hidden 1536, 24/8 heads, 40 experts "
-                                f"top-8, intermediate 512), batch {args.batch}, prompt {args.prompt}, "
+        "config": {"workload": (f"{name} decode: {args.model} shape ({cfg.num_hidden_layers} layers, hidden "
+                                f"{cfg.hidden_size}, {cfg.num_attention_heads}/{cfg.num_key_value_heads} heads, "
+                                f"{cfg.num_local_experts} experts top-{cfg.num_experts_per_tok}, intermediate "
+                                f"{cfg.intermediate_size}), batch {args.batch}, prompt {args.prompt}, "
                                 f"{args.new_tokens} new tokens, greedy, one hipGraph per decode step"),
                    "global_batch": args.batch, "seq_len": args.prompt, "new_tokens": args.new_tokens,
                    "capacity": engine.capacity, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "gate_up_scan_kernel (lm_moe_gate_up)",
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("gate_up_scan_kernel.granite3b_b64_decode.txt"),
+                     "traffic": measured_traffic("gate_up_scan_kernel.granite3b_b64_decode.txt") if headline else None,
                      "bytes_per_launch": int(roof["gate_up_bytes"]), "us_per_launch": round(roof["gate_up_us"], 2),
                      "active_experts": roof["active"]},
         "fused_moe": {"achieved": round(fused_gbs, 1), "unit": "GB/s", "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
