@@ -139,12 +139,16 @@ int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1,
  * flash_decode.py:16-22). qkv_partials: fp32 [qkv_splits][batch][(q_heads +
  * 2*kv_heads) * 64] (q heads, then k, then v); 1 <= qkv_splits <= 8;
  * cos_sin, table_len, positions, active as lm_rope_kv_write (active may be
- * NULL: every row writes). Other arguments and the workspace as
- * lm_flash_decode. */
+ * NULL: every row writes). row_order (int32 [batch], may be NULL): a
+ * permutation of the rows, the order in which their workgroups are
+ * dispatched (lm_decode_prologue writes rows by descending used, so that a
+ * ragged batch does not end on a tail of long rows); results do not depend
+ * on it. Other arguments and the workspace as lm_flash_decode. */
 int lm_flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits,
                         const void *cos_sin, int64_t table_len,
                         const int64_t *positions, const uint8_t *active,
                         void *k_cache, void *v_cache, const int32_t *used,
+                        const int32_t *row_order,
                         int64_t batch, int64_t q_heads, int64_t kv_heads,
                         int64_t capacity, int64_t head_dim, float scale,
                         int64_t max_len, int64_t num_splits, void *out,
@@ -379,13 +383,16 @@ int lm_moe_finish_add_rmsnorm(const void *y, const int32_t *ids,
  * (used, lean decode), :104 (embedding) and :106 (first layer's norm,
  * lm_rmsnorm's rounding). active/valid are bool bytes; length/next int64;
  * next is clamped to [0, vocab). hidden a multiple of 8, at most 4096
- * (else LM_EUNSUPPORTED). */
+ * (else LM_EUNSUPPORTED). row_order (int32 [rows], may be NULL): the rows
+ * by descending used, equal used by ascending row (the stable argsort of
+ * -used), for lm_flash_decode_qkv's dispatch order. No counterpart in the
+ * reference, whose attention kernel schedules itself. */
 int lm_decode_prologue(const uint8_t *active, const int64_t *length,
                        const int64_t *next, const void *embedding,
                        float multiplier, const void *norm_weight, float eps,
                        void *x, void *z, uint8_t *valid, int64_t *positions,
-                       int32_t *used, int64_t rows, int64_t hidden,
-                       int64_t vocab, void *stream);
+                       int32_t *used, int32_t *row_order, int64_t rows,
+                       int64_t hidden, int64_t vocab, void *stream);
 
 /* The end of one greedy decode step, per row b (one launch):
  *   candidate = argmax_v bf16(logits[b][v] * (1 / logits_scaling)), the

@@ -75,6 +75,7 @@ struct QkvIn {
   int64_t table_len;
   const int64_t *pos;     // [batch] position of the new key
   const uint8_t *active;  // [batch] or NULL (all rows write)
+  const int32_t *order;   // [batch] row of workgroup z (longest first), or NULL: row z
 };
 
 constexpr int kMaxQkvSplits = 8;
@@ -101,7 +102,10 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
   __shared__ float sm_qkv[kFused ? G + 2 : 1][kD];
   __shared__ u32x4 sm_knew[kFused ? kLanesPerKey : 1];  // rotated new key, bf16 words per lane group
   const int split = blockIdx.x, h = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  // Workgroups are dispatched in z order; with a row order (rows by
+  // descending length) the longest rows start first and a ragged batch ends
+  // on short rows instead of a tail of long ones.
+  const int64_t b = kFused && in.order ? in.order[blockIdx.z] : blockIdx.z;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int ks = lane / kLanesPerKey, dc = lane % kLanesPerKey;
   // Fused: this row's q|k|v slices of the packed projection, summed over the
@@ -484,7 +488,7 @@ extern "C" int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1, const vo
   if (head_dim != kD) return LM_EUNSUPPORTED;
   if (batch == 0) return LM_OK;
   LM_REQUIRE(q && k_cache && v_cache && used && out);
-  const QkvIn in{nullptr, 0, nullptr, 0, nullptr, nullptr};
+  const QkvIn in{nullptr, 0, nullptr, 0, nullptr, nullptr, nullptr};
   return launch_decode(q, qs0, qs1, const_cast<void *>(k_cache), const_cast<void *>(v_cache),
                        used, batch, q_heads, kv_heads, capacity, scale, max_len, num_splits, in,
                        out, workspace, workspace_bytes_, stream);
@@ -494,7 +498,8 @@ extern "C" int lm_flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits
                                    const void *cos_sin, int64_t table_len,
                                    const int64_t *positions, const uint8_t *active,
                                    void *k_cache, void *v_cache, const int32_t *used,
-                                   int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                   const int32_t *row_order, int64_t batch, int64_t q_heads,
+                                   int64_t kv_heads,
                                    int64_t capacity, int64_t head_dim, float scale,
                                    int64_t max_len, int64_t num_splits, void *out,
                                    void *workspace, int64_t workspace_bytes_, void *stream) {
@@ -504,7 +509,7 @@ extern "C" int lm_flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits
   if (batch == 0) return LM_OK;
   LM_REQUIRE(qkv_partials && cos_sin && positions && k_cache && v_cache && used && out);
   const QkvIn in{qkv_partials, (int)qkv_splits, (const bf16 *)cos_sin, table_len, positions,
-                 active};
+                 active, row_order};
   return launch_decode(nullptr, 0, 0, k_cache, v_cache, used, batch, q_heads, kv_heads, capacity,
                        scale, max_len, num_splits, in, out, workspace, workspace_bytes_, stream);
 }

@@ -26,9 +26,10 @@ prologue_kernel(const uint8_t *__restrict__ active, const int64_t *__restrict__ 
                 const int64_t *__restrict__ next, const bf16 *__restrict__ table, float multiplier,
                 const bf16 *__restrict__ nw, float eps, bf16 *__restrict__ x,
                 bf16 *__restrict__ z, uint8_t *__restrict__ valid,
-                int64_t *__restrict__ positions, int32_t *__restrict__ used, int hidden,
-                int64_t vocab) {
+                int64_t *__restrict__ positions, int32_t *__restrict__ used,
+                int32_t *__restrict__ order, int hidden, int64_t vocab) {
   __shared__ float red[kThreads / kWave];
+  __shared__ float rank_red[kThreads / kWave];
   const int64_t row = blockIdx.x;
   const int nvec = hidden / 8;
   const int64_t tok = min(max(next[row], (int64_t)0), vocab - 1);
@@ -46,6 +47,27 @@ prologue_kernel(const uint8_t *__restrict__ active, const int64_t *__restrict__ 
     valid[row] = act;
     positions[row] = pos;
     used[row] = (int32_t)(pos + 1);
+  }
+  if (order) {
+    // This row's rank among all rows by descending used (equal used: lower
+    // row first), i.e. order = the stable argsort of -used; the decode
+    // attention runs its workgroups in that order.
+    const int rows = (int)gridDim.x;
+    const int64_t mine = active[row] ? length[row] + 1 : 1;
+    float cnt = 0.f;  // exact below 2^24
+    for (int j = threadIdx.x; j < rows; j += kThreads) {
+      const int64_t u = active[j] ? length[j] + 1 : 1;
+      cnt += (u > mine || (u == mine && j < row)) ? 1.f : 0.f;
+    }
+    cnt = wave_sum(cnt);
+    if (threadIdx.x % kWave == 0) rank_red[threadIdx.x / kWave] = cnt;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float r = 0.f;
+#pragma unroll
+      for (int w = 0; w < kThreads / kWave; ++w) r += rank_red[w];
+      order[(int)r] = (int32_t)row;
+    }
   }
   float xn[kMaxVec][8];
   float ss = 0.f;
@@ -216,8 +238,8 @@ using namespace lm;
 extern "C" int lm_decode_prologue(const uint8_t *active, const int64_t *length, const int64_t *next,
                                   const void *embedding, float multiplier, const void *norm_weight,
                                   float eps, void *x, void *z, uint8_t *valid, int64_t *positions,
-                                  int32_t *used, int64_t rows, int64_t hidden, int64_t vocab,
-                                  void *stream) {
+                                  int32_t *used, int32_t *row_order, int64_t rows, int64_t hidden,
+                                  int64_t vocab, void *stream) {
   LM_REQUIRE(rows >= 0 && hidden > 0 && vocab > 0);
   if (hidden % 8 || hidden > kMaxVec * 8 * kThreads) return LM_EUNSUPPORTED;
   if (rows == 0) return LM_OK;
@@ -225,7 +247,7 @@ extern "C" int lm_decode_prologue(const uint8_t *active, const int64_t *length, 
              positions && used);
   prologue_kernel<<<dim3((unsigned)rows), kThreads, 0, (hipStream_t)stream>>>(
       active, length, next, (const bf16 *)embedding, multiplier, (const bf16 *)norm_weight, eps,
-      (bf16 *)x, (bf16 *)z, valid, positions, used, (int)hidden, vocab);
+      (bf16 *)x, (bf16 *)z, valid, positions, used, row_order, (int)hidden, vocab);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

@@ -27,7 +27,7 @@ def default_splits(batch, kv_heads, maximum, target_workgroups=512, min_keys=256
 
 
 class FlashDecode:
-    def __init__(self, batch, kv_heads, groups, capacity, device, maximum=None, num_splits=None):
+    def __init__(self, batch, kv_heads, groups, capacity, device, maximum=None, num_splits=None, ordered=False):
         if maximum is not None and not 0 < maximum <= capacity:
             raise ValueError("Decode attention requires a valid length bound")
         self.batch, self.kv_heads, self.groups, self.capacity = batch, kv_heads, groups, capacity
@@ -37,6 +37,10 @@ class FlashDecode:
         size = _lib.size_query("lm_flash_decode_workspace_size", batch, kv_heads * groups, 64,
                                self.splits) if self.device.type == "cuda" else 0
         self.workspace = torch.empty(max(size, 1), dtype=torch.uint8, device=self.device)
+        # ordered: a dispatch order (rows by descending length) the decode
+        # prologue fills each step, for ragged batches (see fused_qkv).
+        self.row_order = (torch.empty(batch, dtype=torch.int32, device=self.device)
+                          if ordered and self.device.type == "cuda" else None)
 
     def __call__(self, q, k, v, lengths, active, scale, used=None):
         b, hq, s, d = q.shape
@@ -61,12 +65,14 @@ class FlashDecode:
                   _lib.stream(q.device))
         return out
 
-    def fused_qkv(self, partials, cos_sin, positions, active, k, v, scale, used, q_heads):
+    def fused_qkv(self, partials, cos_sin, positions, active, k, v, scale, used, q_heads, row_order=None):
         """Attention of one new token per row from the packed QKV projection's
         partials ``[S, B, (Hq + 2 Hkv) * 64]`` (litemoe/model.py:47-71 after
         the projection). Writes the rotated key and the value at
         ``positions[b]`` of ``k``/``v`` (rows with ``active`` false, when
-        given, write nothing) and returns ``[B, Hq, 1, 64]``."""
+        given, write nothing) and returns ``[B, Hq, 1, 64]``. ``row_order``
+        (int32 ``[B]``, a permutation of the rows) sets the order in which the
+        rows' workgroups are dispatched; results do not depend on it."""
         splits, b, ncols = partials.shape
         hkv = k.shape[1]
         if ncols != (q_heads + 2 * hkv) * 64 or q_heads % hkv or k.shape != v.shape:
@@ -85,8 +91,11 @@ class FlashDecode:
             # a bool mask is one byte per row: read it in place (no conversion launch)
             act = (active.view(torch.uint8) if active.dtype == torch.bool else active.to(torch.uint8)).contiguous()
         out = torch.empty(b, q_heads, 1, 64, device=k.device, dtype=k.dtype)
+        if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (b,)):
+            raise ValueError("row_order must be an int32 [B] permutation")
         _lib.call("lm_flash_decode_qkv", partials.data_ptr(), splits, cos_sin.data_ptr(), cos_sin.shape[0],
-                  positions.data_ptr(), _lib.ptr(act), k.data_ptr(), v.data_ptr(), used.data_ptr(), b,
+                  positions.data_ptr(), _lib.ptr(act), k.data_ptr(), v.data_ptr(), used.data_ptr(),
+                  _lib.ptr(row_order), b,
                   q_heads, hkv, self.capacity, 64, float(scale), self.maximum, self.splits,
                   out.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(), _lib.stream(k.device))
         return out

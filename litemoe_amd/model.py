@@ -50,6 +50,7 @@ class Granite:
         self.decode_flash = None   # FlashDecode set by the execution policy
         self.decode_lean = False   # positions pre-zeroed for stopped rows; outputs unmasked
         self.used = None
+        self._row_order = None     # the decode prologue's row order, during greedy_step only
         self._flash = {}
         device, dtype = weights["embedding"].device, weights["embedding"].dtype
         dim = cfg.hidden_size // cfg.num_attention_heads
@@ -122,8 +123,9 @@ class Granite:
         rows = z.shape[0]
         part = linear_splitk(z, w["self_attn.qkv_proj"], splits[0])
         flash = self._decode_attention(rows, cache)
+        order = self._row_order if self._row_order is not None and self._row_order.shape[0] == rows else None
         a = flash.fused_qkv(part, self.cos_sin, rope_positions, active, cache.k[layer], cache.v[layer],
-                            cfg.attention_multiplier, self.used, cfg.num_attention_heads)
+                            cfg.attention_multiplier, self.used, cfg.num_attention_heads, row_order=order)
         return linear_splitk(a.view(rows, -1), w["self_attn.o_proj"], splits[1])
 
     def _fused_moe(self):
@@ -170,11 +172,19 @@ class Granite:
         Same tokens and state as litemoe/engine.py:87-102 around this model's
         forward (model.py:95-127) in lean decode."""
         cfg = self.cfg
+        order = getattr(self.decode_flash, "row_order", None)
+        if order is not None and order.shape[0] != state["active"].shape[0]:
+            order = None
         x, z, valid, positions, used = decode_prologue(
             state["active"], state["length"], state["next"], self.w["embedding"],
-            cfg.embedding_multiplier, self.w["layers"][0]["input_layernorm"], cfg.rms_norm_eps)
+            cfg.embedding_multiplier, self.w["layers"][0]["input_layernorm"], cfg.rms_norm_eps,
+            row_order=order)
         self.used = used
-        z = self._fused_layers(x, z, cache, positions, valid, positions, None)
+        self._row_order = order  # valid for this step only: the prologue just wrote it
+        try:
+            z = self._fused_layers(x, z, cache, positions, valid, positions, None)
+        finally:
+            self._row_order = None
         greedy_epilogue(F.linear(z, self.w["head"]), cfg.logits_scaling, valid, state, emit, eos,
                         ignore_eos)
 

@@ -47,9 +47,14 @@ class OptimizedEngine(Engine):
         self.flash_attention = None
         if self.requests:
             maximum = max(len(r.prompt) + r.budget - 1 for r in self.requests)
+            # A ragged batch (the longest prompt more than 1.25x the shortest)
+            # dispatches its attention rows longest first.
+            lengths = [len(r.prompt) for r in self.requests]
+            ragged = max(lengths) > 1.25 * min(lengths)
             self.flash_attention = FlashDecode(self.batch, cfg.num_key_value_heads,
                                                cfg.num_attention_heads // cfg.num_key_value_heads,
-                                               self.capacity, self.device, maximum, num_splits)
+                                               self.capacity, self.device, maximum, num_splits,
+                                               ordered=ragged)
 
     def prepare_graph(self):
         with optimized_policy(self):

@@ -19,12 +19,14 @@ def _bool_bytes(t):
     return t.view(torch.uint8)
 
 
-def decode_prologue(active, length, next_tokens, embedding, multiplier, norm_weight, eps):
+def decode_prologue(active, length, next_tokens, embedding, multiplier, norm_weight, eps, row_order=None):
     """Returns ``(x, z, valid, positions, used)`` for one decode step.
 
     ``valid = active``; ``positions = where(valid, length, 0)``;
     ``used = int32(positions + 1)``; ``x = embedding[next] * multiplier``
-    (bf16); ``z = rmsnorm(x, norm_weight, eps)``.
+    (bf16); ``z = rmsnorm(x, norm_weight, eps)``. With ``row_order`` (int32
+    ``[rows]``) also the rows by descending ``used`` (ties by row), the
+    dispatch order for :meth:`FlashDecode.fused_qkv`.
     """
     _lib.require_cuda(active, length, next_tokens, embedding, norm_weight, what="decode prologue inputs")
     rows = active.shape[0]
@@ -42,10 +44,14 @@ def decode_prologue(active, length, next_tokens, embedding, multiplier, norm_wei
     valid = torch.empty(rows, dtype=torch.bool, device=dev)
     positions = torch.empty(rows, dtype=torch.int64, device=dev)
     used = torch.empty(rows, dtype=torch.int32, device=dev)
+    if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (rows,)
+                                  or not row_order.is_contiguous()):
+        raise ValueError("row_order must be a contiguous int32 [rows] tensor")
     _lib.call("lm_decode_prologue", _bool_bytes(active).data_ptr(), length.data_ptr(),
               next_tokens.data_ptr(), embedding.data_ptr(), float(multiplier), norm_weight.data_ptr(),
               float(eps), x.data_ptr(), z.data_ptr(), valid.view(torch.uint8).data_ptr(),
-              positions.data_ptr(), used.data_ptr(), rows, hidden, vocab, _lib.stream(dev))
+              positions.data_ptr(), used.data_ptr(), _lib.ptr(row_order), rows, hidden, vocab,
+              _lib.stream(dev))
     return x, z, valid, positions, used
 
 

@@ -104,6 +104,16 @@ def test_flash_decode_qkv_equals_unfused(b, hq, hkv, cap, attn_splits, qkv_split
     got = fd.fused_qkv(part, cos_sin, pos, active, caches[1].k[0], caches[1].v[0], 0.125, used, hq)
     assert torch.equal(got, exp)
     assert torch.equal(caches[1].k, caches[0].k) and torch.equal(caches[1].v, caches[0].v)
+    # any dispatch order of the rows gives the same bits (a fresh copy of the
+    # cache: the fused call writes the new keys again)
+    g = torch.Generator().manual_seed(b)
+    order = torch.randperm(b, generator=g).to(torch.int32).to(DEV)
+    caches[1].k.copy_(caches[0].k)
+    caches[1].v.copy_(caches[0].v)
+    got2 = fd.fused_qkv(part, cos_sin, pos, active, caches[1].k[0], caches[1].v[0], 0.125, used, hq,
+                        row_order=order)
+    assert torch.equal(got2, got)
+    assert torch.equal(caches[1].k, caches[0].k) and torch.equal(caches[1].v, caches[0].v)
     # and against the oracle's attention over the updated cache
     rows = list(range(min(b, 8)))
     ref = ops.decode_attention(q.cpu()[rows], caches[0].k[0].cpu()[rows], caches[0].v[0].cpu()[rows],

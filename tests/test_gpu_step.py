@@ -54,6 +54,26 @@ def test_prologue_equals_reference_ops(rows, vocab, hidden):
     assert torch.equal(z, norm.rmsnorm(ex.contiguous(), weight, eps))
 
 
+@pytest.mark.parametrize("rows", [1, 7, 64, 300])
+@torch.inference_mode()
+def test_prologue_row_order_is_stable_argsort_of_used(rows):
+    """The dispatch order the prologue writes for the decode attention: rows
+    by descending used, equal used by ascending row."""
+    s = state_for(rows, 100, rows)
+    s["length"] = (s["length"] % 7).to(DEV)  # many ties
+    table = normal_bf16((100, 256), 0.5, 1).to(DEV)
+    weight = torch.ones(256, dtype=torch.bfloat16, device=DEV)
+    order = torch.full((rows,), -1, dtype=torch.int32, device=DEV)
+    out = step.decode_prologue(s["active"], s["length"], s["next"], table, 1.0, weight, 1e-6, row_order=order)
+    used = out[4].cpu().long()
+    expect = torch.sort(-used, stable=True).indices.to(torch.int32)
+    assert torch.equal(order.cpu(), expect)
+    # and the other outputs are unchanged by it
+    ref = step.decode_prologue(s["active"], s["length"], s["next"], table, 1.0, weight, 1e-6)
+    for a, b in zip(out, ref):
+        assert torch.equal(a, b)
+
+
 @torch.inference_mode()
 def test_prologue_limits():
     s = state_for(2, 10, 1)
