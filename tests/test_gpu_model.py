@@ -175,31 +175,40 @@ def test_granite_1b_shape_layer_graph_replay_is_deterministic():
         assert run_g.generate()[0] == eager
 
 
+@pytest.mark.parametrize("name,batch,lengths,capacity", [
+    ("granite-3b", 64, 1024, 2048),                   # cfg 3, the headline configuration
+    ("granite-1b", 32, 512, 1024),                    # cfg 2
+    ("granite-3b", 128, (1024, 4032, 3), 4096)])      # cfg 5: ragged, rows dispatched longest first
 @torch.inference_mode()
-def test_full_cfg3_graph_replay_equals_eager():
-    """The headline configuration at full size (Granite-3B shape, all 32
-    layers, vocab 49155, batch 64, prompts of 1024 tokens): the hipGraph
-    decode replays give the eager tokens, state and KV cache bit for bit,
-    on two generate() calls; every emitted token is in the vocabulary."""
+def test_full_size_graph_replay_equals_eager(name, batch, lengths, capacity):
+    """The benchmark configurations at full size (all layers, vocab 49155):
+    the hipGraph decode replays give the eager tokens, state and KV cache
+    bit for bit, on two generate() calls; every emitted token is in the
+    vocabulary."""
     from litemoe_amd import synth
     from litemoe_amd.config import preset
-    cfg = preset("granite-3b")
+    cfg = preset(name)
+    if isinstance(lengths, tuple):
+        lengths = synth.ragged_lengths(batch, *lengths)
     w = synth.granite_weights(cfg, seed=0, device=DEV, method="torch")
-    ep = ExpertParallel(1, 0, 64 * 1024, cfg.hidden_size, cfg.num_experts_per_tok, torch.bfloat16, DEV,
+    total = lengths * batch if isinstance(lengths, int) else sum(lengths)
+    ep = ExpertParallel(1, 0, total, cfg.hidden_size, cfg.num_experts_per_tok, torch.bfloat16, DEV,
                         HipFusedExperts())
-    model = Granite(cfg, w, ep, 2048)
-    prompts = synth.prompts(64, 1024, cfg.vocab_size, 1)
+    model = Granite(cfg, w, ep, capacity)
+    prompts = synth.prompts(batch, lengths, cfg.vocab_size, 1)
     requests = [Request(str(i), p, 5) for i, p in enumerate(prompts)]
-    eager_run = OptimizedEngine(model, requests, ignore_eos=True, capacity=2048)
+    eager_run = OptimizedEngine(model, requests, ignore_eos=True, capacity=capacity)
     eager, _ = eager_run.generate()
     assert all(len(t) == 5 and all(0 <= x < cfg.vocab_size for x in t) for t in eager.values())
-    graph_run = OptimizedEngine(model, requests, ignore_eos=True, capacity=2048, mode="graph")
+    graph_run = OptimizedEngine(model, requests, ignore_eos=True, capacity=capacity, mode="graph")
     for _ in range(2):
         actual, metrics = graph_run.generate()
         assert actual == eager
-        assert metrics["output_tokens"] == 64 * 5
+        assert metrics["output_tokens"] == batch * 5
         for k in eager_run.state:
             assert torch.equal(graph_run.state[k], eager_run.state[k]), k
         assert torch.equal(graph_run.cache.k, eager_run.cache.k)
         assert torch.equal(graph_run.cache.v, eager_run.cache.v)
+    del eager_run, graph_run, model, w
+    torch.cuda.empty_cache()
 
