@@ -139,8 +139,8 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
         p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[h][i], sl2, -mn));  // exp2(-inf) = 0; mn is finite
         rs += p[i];
       }
-      pw[2 * h] = pack_bf16(p[0], p[1]);
-      pw[2 * h + 1] = pack_bf16(p[2], p[3]);
+      pw[2 * h] = pack_bf16_finite(p[0], p[1]);  // p = exp2(finite or -inf): never NaN
+      pw[2 * h + 1] = pack_bf16_finite(p[2], p[3]);
     }
     rs += shfl_xor(rs, 16);
     rs += shfl_xor(rs, 32);

@@ -36,6 +36,11 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   if (hi != hi) h = (h & 0xffffu) | 0x7fc00000u;
   return h;
 }
+// pack_bf16 for values known not to be NaN (e.g. exp2 of a finite or -inf
+// argument): the conversion alone, the same bits.
+__device__ __forceinline__ uint32_t pack_bf16_finite(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   const uint32_t h = __builtin_bit_cast(uint16_t, (__bf16)f);
   return f != f ? 0x7fc0u : h;
