@@ -23,7 +23,8 @@ namespace {
 constexpr int kD = 64;
 constexpr int kThreads = 256;
 constexpr int kBQ = 64;
-constexpr int kBK = 32;
+constexpr int kBK = 64;
+constexpr int kStage = kBK / 32;  // keys each staging thread loads per tile (one per 32)
 constexpr int kKPad = 8;
 
 typedef short short4v __attribute__((ext_vector_type(4)));
@@ -79,28 +80,35 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
   const int skey = threadIdx.x / 8, sdc = threadIdx.x % 8;
   const bf16 *kbase = k + (int64_t)start * ks0 + (int64_t)hk * ks1 + sdc * 8;
   const bf16 *vbase = v + (int64_t)start * vs0 + (int64_t)hk * vs1 + sdc * 8;
-  auto load = [&](int kt, u32x4 &kv, u32x4 &vv) {
-    const int64_t row = min(kt + skey, len - 1);
-    kv = *reinterpret_cast<const u32x4 *>(kbase + row * ks0);
-    vv = *reinterpret_cast<const u32x4 *>(vbase + row * vs0);
+  auto load = [&](int kt, u32x4 *kv, u32x4 *vv) {
+#pragma unroll
+    for (int r = 0; r < kStage; ++r) {
+      const int64_t row = min(kt + skey + 32 * r, len - 1);
+      kv[r] = *reinterpret_cast<const u32x4 *>(kbase + row * ks0);
+      vv[r] = *reinterpret_cast<const u32x4 *>(vbase + row * vs0);
+    }
   };
   // Transposing-read addresses: lane 16g + 4j + t reads channels 4t..4t+3
   // (plus 16 per channel block) of key row 4g + j (slots 0-3) or
   // 16 + 4g + j (slots 4-7), matching the keys of the P fragment.
   const int trow = 4 * grp + (col / 4), tch = 4 * (col % 4);
-  u32x4 kv, vv;
+  u32x4 kv[kStage], vv[kStage];
   load(0, kv, vv);
   for (int kt = 0; kt < kend; kt += kBK) {
     __syncthreads();  // the previous tile is no longer read
-    *reinterpret_cast<u32x4 *>(&ks_lds[skey][sdc * 8]) = kv;
-    *reinterpret_cast<u32x4 *>(&vs_lds[skey][sdc * 8]) = vv;
+#pragma unroll
+    for (int r = 0; r < kStage; ++r) {
+      *reinterpret_cast<u32x4 *>(&ks_lds[skey + 32 * r][sdc * 8]) = kv[r];
+      *reinterpret_cast<u32x4 *>(&vs_lds[skey + 32 * r][sdc * 8]) = vv[r];
+    }
     __syncthreads();
     // The next tile streams in while this one is computed.
     load(min(kt + kBK, kend - 1), kv, vv);
     if (!wave_live || (causal && kt > wq0 + 15)) continue;
-    f32x4 st[2];
+    constexpr int kH = kBK / 16;  // 16-key blocks of the tile
+    f32x4 st[kH];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kH; ++h) {
       const u32x4 a0 = *reinterpret_cast<const u32x4 *>(&ks_lds[16 * h + col][grp * 8]);
       const u32x4 a1 = *reinterpret_cast<const u32x4 *>(&ks_lds[16 * h + col][32 + grp * 8]);
       st[h] = mfma16x16x32(a0, qf0, f32x4{0.f, 0.f, 0.f, 0.f});
@@ -111,7 +119,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     const bool masking = kt + kBK > len || (causal && kt + kBK - 1 > wq0);
     if (masking) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < kH; ++h)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int j = kt + 16 * h + grp * 4 + i;
@@ -122,7 +130,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     // and exp2(s * scale*log2e - m) is one FMA and one v_exp_f32.
     float mt = -INFINITY;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < kH; ++h)
 #pragma unroll
       for (int i = 0; i < 4; ++i) mt = fmaxf(mt, st[h][i]);
     mt = fmaxf(mt, shfl_xor(mt, 16));
@@ -130,9 +138,9 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     const float mn = fmaxf(m, mt * sl2);
     const float corr = factor(m, mn);
     float rs = 0.f;
-    uint32_t pw[4];
+    uint32_t pw[2 * kH];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kH; ++h) {
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -146,7 +154,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     rs += shfl_xor(rs, 32);
     l = l * corr + rs;
     m = mn;
-    const u32x4 pa = {pw[0], pw[1], pw[2], pw[3]};
+
     // O rows held by this lane are queries 4*grp + i of the wave; the
     // rescale is skipped when no query of the wave moved its maximum.
     if (__ballot(corr != 1.f)) {
@@ -158,12 +166,18 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[d][i] *= rc[i];
     }
+    // Each 32 keys of the tile are one P.V step: keys 32c + (the two
+    // 16-key blocks' rows) as the eight k slots.
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint2 lo = read_tr(&vs_lds[trow][d * 16 + tch]);
-      const uint2 hi = read_tr(&vs_lds[16 + trow][d * 16 + tch]);
-      const u32x4 vb = {lo.x, lo.y, hi.x, hi.y};
-      o[d] = mfma16x16x32(pa, vb, o[d]);
+    for (int c = 0; c < kBK / 32; ++c) {
+      const u32x4 pa = {pw[4 * c], pw[4 * c + 1], pw[4 * c + 2], pw[4 * c + 3]};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint2 lo = read_tr(&vs_lds[32 * c + trow][d * 16 + tch]);
+        const uint2 hi = read_tr(&vs_lds[32 * c + 16 + trow][d * 16 + tch]);
+        const u32x4 vb = {lo.x, lo.y, hi.x, hi.y};
+        o[d] = mfma16x16x32(pa, vb, o[d]);
+      }
     }
   }
   if (!wave_live) return;
