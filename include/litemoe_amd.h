@@ -79,8 +79,12 @@ int lm_kv_write(const void *k, int64_t ks0, int64_t ks1, int64_t ks3,
 /* Neox rotary embedding on q and k fused with the masked KV store.
  * For every row r (positions[r] indexes cos_sin, [table_len, head_dim] bf16
  * holding cat(cos[:, :D/2], sin[:, :D/2]) as built at litemoe/model.py:31-35):
- *   q[r,h,i]     <- x1*cos - x2*sin,  q[r,h,i+D/2] <- x2*cos + x1*sin
- * with x1 = q[r,h,i], x2 = q[r,h,i+D/2], i < D/2 (fp32 math, one rounding),
+ *   q[r,h,i]     <- bf16( bf16(x1*c) - bf16(x2*s) )
+ *   q[r,h,i+D/2] <- bf16( bf16(x2*c) + bf16(x1*s) )
+ * with x1 = q[r,h,i], x2 = q[r,h,i+D/2], c/s the bf16 table entries, i < D/2:
+ * the three roundings of the reference's bf16 torch formula
+ * `q*cos + rotate_half(q)*sin` (model.py:13-15,66-67; each product and the
+ * sum rounded to bf16, products formed in fp32),
  * and the same rotation of k, which is stored into k_cache at
  * (slot[r], h, pos[r]) under the lm_kv_write mask, v stored unrotated.
  * write_k (nonzero) also writes rotated k back in place (prefill needs it).
@@ -238,7 +242,13 @@ int lm_fused_experts_workspace_size(int64_t tokens, int64_t topk,
  * {1, 2, 3, 4, 6, 8, 12, 16}. block_rows (0 = automatic) is the number of
  * routes one workgroup carries per weight tile (a multiple of 16). logical
  * (int64 [experts] or NULL for identity) only reorders the combine, as in
- * lm_moe_finish. */
+ * lm_moe_finish.
+ * Expert ids are device data, so they are not validated at the call: a token
+ * may list an expert more than once (each route is computed and combined,
+ * as the reference's reference_experts does, litemoe/ops.py:34-55), and a
+ * route whose id lies outside [0, experts) is skipped: it adds nothing to
+ * out and its expert rows are never read (the reference CPU path raises on
+ * such ids; vLLM leaves them undefined). */
 int lm_fused_experts(const void *x, const void *w13, const void *w2,
                      const float *topk_weights, const int32_t *topk_ids,
                      const int64_t *logical, int64_t tokens, int64_t hidden,
@@ -252,10 +262,12 @@ int lm_fused_experts(const void *x, const void *w13, const void *w2,
  *   g/u = W13[e] . x[r / topk]; act is [routes, inter] in route order.
  * down: y[r, :] = bf16(W2[e] . act[r, :]); y is [routes, hidden] in route
  *   order. Routes of the ignored tail are not touched.
- * With topk_ids given (routes <= 2048, at most 256 routes per expert) each
- * expert's workgroups collect
- * its routes themselves and expert_offsets/sorted_routes may be NULL;
- * otherwise the routes come from lm_moe_align's offsets and permutation. */
+ * With topk_ids given (routes <= 2048, routes / topk <= 256 tokens) each
+ * expert's workgroups collect its routes themselves (any number of them,
+ * so repeated ids within a token are computed) and
+ * expert_offsets/sorted_routes may be NULL; otherwise the routes come from
+ * lm_moe_align's offsets and permutation. Routes whose id lies outside
+ * [0, experts) are not computed and their act/y rows are not written. */
 int lm_moe_gate_up(const void *x, const void *w13,
                    const int32_t *expert_offsets, const int32_t *sorted_routes,
                    const int32_t *topk_ids, int64_t routes, int64_t topk,
@@ -353,7 +365,9 @@ int lm_moe_routes_workspace_size(int64_t tokens, int64_t topk, int64_t hidden,
  * themselves (no permutation pass); larger batches use lm_moe_align blocks.
  * Replaces the expert GEMMs inside vLLM fused_experts (litemoe/ep.py:40-41)
  * and the per-expert loop of litemoe/ops.py:43-47. Shapes as
- * lm_fused_experts; y: [tokens*topk, hidden] bf16. */
+ * lm_fused_experts; y: [tokens*topk, hidden] bf16. Repeated ids within a
+ * token are computed on every path; the y rows of routes whose id lies
+ * outside [0, experts) are not written. */
 int lm_moe_routes(const void *x, const void *w13, const void *w2,
                   const int32_t *topk_ids, int64_t tokens, int64_t hidden,
                   int64_t inter, int64_t experts, int64_t topk,
@@ -366,7 +380,8 @@ int lm_moe_routes(const void *x, const void *w13, const void *w2,
  *   z[t] = rmsnorm(x[t], norm_weight).
  * Replaces moe_finish (litemoe/moe_finish.py:7-57) followed by
  * litemoe/model.py:122 and the next layer's :106 (or the final norm :126).
- * logical as lm_moe_finish (NULL = identity). */
+ * logical as lm_moe_finish (NULL = identity). Every route is owned: ids must
+ * lie in [0, experts) (lm_router's ids always do). */
 int lm_moe_finish_add_rmsnorm(const void *y, const int32_t *ids,
                               const float *scales, const int64_t *logical,
                               void *x, float alpha, const void *norm_weight,

@@ -20,13 +20,17 @@ finish_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ ids,
   const int64_t t = blockIdx.x;
   const int c0 = (blockIdx.y * 256 + threadIdx.x) * kCols;
   if (c0 >= hidden) return;
-  // Rank of each branch under the key logical*K + j (keys are distinct).
+  // Rank of each branch under the key logical*K + j (keys are distinct:
+  // j differs). A route that is not owned adds nothing wherever it ranks, so
+  // its key uses the raw id and the map is read for owned ids only (an id
+  // outside every rank's range never indexes it).
   int64_t key[kMaxK];
 #pragma unroll
   for (int j = 0; j < kMaxK; ++j) {
     if (j < topk) {
       const int64_t e = ids[t * topk + j];
-      key[j] = (logical ? logical[e] : e) * topk + j;
+      const bool owned = e - rank * count >= 0 && e - rank * count < count;
+      key[j] = (logical && owned ? logical[e] : e) * topk + j;
     } else {
       key[j] = INT64_MAX;
     }

@@ -29,7 +29,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kMaxScanRows = 256;
+constexpr int kMaxScanRows = 256;  // tokens of a call on the scan path
 
 // How a workgroup finds its routes and when it loads its weight tile.
 enum RouteMode : int {
@@ -63,6 +63,9 @@ __device__ __forceinline__ bool find_block(const int32_t *__restrict__ offsets, 
 // Wave w owns routes [w*seg, (w+1)*seg), seg a multiple of 64, at most
 // kScanIters loads of 64 ids per lane.
 constexpr int kScanIters = 8;  // routes <= kWaves * kScanIters * 64 = 2048
+// The LDS route list holds every route of the call, so an expert listed
+// more than once by a token (more than `tokens` routes) still fits.
+constexpr int kScanList = kWaves * kScanIters * kWave;
 
 struct ScanIds {
   int id[kScanIters];  // ids[begin + it*64 + lane], valid below end
@@ -107,11 +110,11 @@ __device__ int scan_ids(const ScanIds &s, int e, int *list, int *wave_count) {
     const bool hit = s.id[it] == e && s.begin + it * kWave + lane < s.end;
     const uint64_t mask = __ballot(hit);
     const int slot = offset + __popcll(mask & below);
-    if (hit && slot < kMaxScanRows) list[slot] = s.begin + it * kWave + lane;
+    if (hit) list[slot] = s.begin + it * kWave + lane;  // slot < total <= routes <= kScanList
     offset += __popcll(mask);
   }
   __syncthreads();
-  return min(total, kMaxScanRows);  // a token picks an expert once: total <= tokens
+  return total;
 }
 
 __device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
@@ -133,7 +136,7 @@ gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
                int experts, int bm, bf16 *__restrict__ act) {
   constexpr bool kScan = kMode != kBlocks;
   __shared__ float red[kWaves][2][4][kWave];
-  __shared__ int list[kScan ? kMaxScanRows : 1];
+  __shared__ int list[kScan ? kScanList : 1];
   __shared__ int wave_count[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
@@ -224,7 +227,7 @@ gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
                     const int32_t *__restrict__ ids, int routes, int topk, int hidden, int inter,
                     bf16 *__restrict__ act) {
   __shared__ float red[kWaves][2][4][kWave];
-  __shared__ int list[kMaxScanRows];
+  __shared__ int list[kScanList];
   __shared__ int wave_count[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
@@ -290,7 +293,7 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
             bf16 *__restrict__ y) {
   constexpr bool kScan = kMode != kBlocks;
   __shared__ float red[kWaves][2][4][kWave];
-  __shared__ int list[kScan ? kMaxScanRows : 1];
+  __shared__ int list[kScan ? kScanList : 1];
   __shared__ int wave_count[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
@@ -381,7 +384,7 @@ down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
                  const int32_t *__restrict__ ids, int routes, int hidden, int inter,
                  bf16 *__restrict__ y) {
   __shared__ float red[kWaves][NT][4][kWave];
-  __shared__ int list[kMaxScanRows];
+  __shared__ int list[kScanList];
   __shared__ int wave_count[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;

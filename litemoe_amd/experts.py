@@ -23,16 +23,26 @@ def _check_weights(x, w1, w2):
 
 
 class _Workspace:
-    """Grow-only device scratch; allocated before graph capture, then reused."""
+    """Grow-only device scratch.
+
+    A captured HIP graph keeps the address of every buffer its kernels were
+    given, so a buffer is never released once handed out: growing allocates
+    a larger one and keeps the old one referenced (``retired``) for the
+    workspace's lifetime. Growth is geometric, so the retired buffers add at
+    most the size of the current one."""
 
     def __init__(self):
         self.buffers = {}
+        self.retired = []
 
     def get(self, device, nbytes):
-        key = (str(device),)
+        key = str(torch.device(device))
         buf = self.buffers.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            size = max(nbytes, 256, 0 if buf is None else 2 * buf.numel())
+            if buf is not None:
+                self.retired.append(buf)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
             self.buffers[key] = buf
         return buf
 

@@ -226,12 +226,18 @@ class Granite:
                     a = a * valid_rows[:, None]
                 add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps, out=z)
                 scales, ids = route(z, w["block_sparse_moe.router.layer"], cfg.num_experts_per_tok)
+                if packed or not self.decode_lean:
+                    # outside the fused paths the reference hands the experts
+                    # bf16 scales (litemoe/model.py:117-118)
+                    scales = scales.to(torch.bfloat16)
                 y = self.ep(z, ids, scales, valid_rows, w["physical"], w["input_linear"], w["output_linear"],
                             w["logical"], decode=True, tokens=communication_tokens)
             z = add_rmsnorm(x, y, r, self.w["norm"], eps, out=z)
         if last is not None:
-            index = last.long() if isinstance(last, torch.Tensor) else torch.tensor([last], device=x.device)
-            z = z[index]
+            # row i keeps position last[i] (litemoe/model.py:123-125); a packed
+            # batch is one row, so its `last` are flat token indices
+            last = last.long() if isinstance(last, torch.Tensor) else torch.tensor(last, device=x.device)
+            z = z[torch.arange(b, device=x.device) * s + last]
             out_rows = (z.shape[0], 1)
         else:
             out_rows = (b, s)

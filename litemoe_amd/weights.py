@@ -103,9 +103,11 @@ def load_weights(cfg, source, placement=None, rank=0, device="cuda", dtype=torch
     """The weight dict ``Granite`` takes (litemoe/weights.py:80-108).
 
     One GPU holds every expert: ``placement`` may be None or a placement of
-    world size 1; a placement that reorders experts keeps its physical
-    order, and ``logical`` is then its inverse permutation, as the
-    reference builds it. ``backend`` is accepted for signature compatibility
+    world size 1. ``placement.physical[layer][e]`` is the slot of checkpoint
+    expert ``e`` (the router's ids are mapped through it before the expert
+    GEMMs), so slot ``s`` is filled with expert ``argsort(physical)[s]`` and
+    ``logical`` is that inverse permutation, as the reference builds it
+    (litemoe/placement.py:31-38, weights.py:92-105). ``backend`` is accepted for signature compatibility
     and not used (the reference passes it through unused as well)."""
     validate_config(cfg)
     layers_n, experts = cfg.num_hidden_layers, cfg.num_local_experts
@@ -137,7 +139,8 @@ def load_weights(cfg, source, placement=None, rank=0, device="cuda", dtype=torch
                 weights[name] = value.to(device=device, dtype=dtype).contiguous()
             else:
                 target = torch.empty(shape, dtype=dtype, device=device)
-                for local, logical in enumerate(physical):
+                holder = sorted(range(experts), key=physical.__getitem__)  # slot -> expert
+                for local, logical in enumerate(holder):
                     value = source.get(key, expert=logical)
                     if tuple(value.shape) != shape[1:]:
                         raise ValueError(f"Checkpoint expert geometry mismatch: {name}")

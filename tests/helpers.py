@@ -70,3 +70,16 @@ def make_hf(seed=7, randomize_norms=True, **geometry):
 def tiny_hf_model():
     hf = make_hf()
     return hf, config_from_hf(hf.config), hf_weights(hf)
+
+
+def bf16_ordered(t):
+    """bf16 bit patterns on a monotone integer line (-0 and +0 coincide)."""
+    i = t.contiguous().view(torch.int16).to(torch.int32)
+    return torch.where(i >= 0, i, -(i & 0x7FFF))
+
+
+def bf16_within_ulp_or_abs(a, b, ulps, floor):
+    """Every element of two bf16 tensors within ``ulps`` units in the last
+    place, or within ``floor`` absolutely (sums near zero cancel)."""
+    close = (bf16_ordered(a) - bf16_ordered(b)).abs() <= ulps
+    return bool((close | ((a.float() - b.float()).abs() <= floor)).all())

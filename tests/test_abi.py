@@ -55,6 +55,45 @@ def test_invalid_arguments_rejected_on_host(call, expected):
     assert call(_lib.load()) == expected
 
 
+# Non-null dummy pointers: every case returns before any launch, so nothing
+# is dereferenced (the checks run on the host only).
+_P = 16
+
+
+@pytest.mark.parametrize("name,call,expected", [
+    ("topk > 8", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 4, 1024, 512, 16, 9, 0, _P, _P, 1 << 30,
+                                                None), 1),
+    ("block_rows % 16", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 4, 1024, 512, 16, 2, 8, _P, _P,
+                                                       1 << 30, None), 1),
+    ("experts > 511", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 4, 1024, 512, 600, 2, 0, _P, _P,
+                                                     1 << 30, None), 1),
+    ("topk > experts", lambda h: h.lm_moe_routes(_P, _P, _P, _P, 4, 1024, 512, 2, 4, 0, _P, _P, 1 << 30, None), 1),
+    ("null workspace", lambda h: h.lm_moe_routes(_P, _P, _P, _P, 4, 1024, 512, 8, 2, 0, _P, None, 1 << 30, None),
+     1),
+    ("workspace short", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 4, 1024, 512, 8, 2, 0, _P, _P, 100,
+                                                       None), 4),
+    ("routes workspace short", lambda h: h.lm_moe_routes(_P, _P, _P, _P, 64, 1536, 512, 40, 8, 0, _P, _P, 4096,
+                                                           None), 4),
+    ("hidden 1000", lambda h: h.lm_moe_routes(_P, _P, _P, _P, 4, 1000, 512, 8, 2, 0, _P, _P, 1 << 30, None), 2),
+    ("scan path > 256 tokens", lambda h: h.lm_moe_gate_up(_P, _P, None, None, _P, 300 * 2, 2, 1024, 512, 8, 0,
+                                                             _P, None), 2),
+    ("splitk rows 129", lambda h: h.lm_linear_splitk(_P, 1536, _P, 129, 2560, 1536, 3, _P, None), 2),
+    ("splitk bad slices", lambda h: h.lm_linear_splitk(_P, 1536, _P, 64, 2560, 1536, 5, _P, None), 2),
+    ("flash workspace short", lambda h: h.lm_flash_decode(_P, 64 * 24, 64, _P, _P, _P, 64, 24, 8, 2048, 64,
+                                                            C.c_float(0.125), 2048, 4, _P, _P, 16, None), 4),
+    ("finish topk 9", lambda h: h.lm_moe_finish(_P, _P, None, _P, None, _P, 1, 8, 9, 0, 1, None, 0, None), 1),
+    ("ok: zero tokens", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 0, 1024, 512, 8, 2, 0, _P, _P, 0,
+                                                       None), 0),
+])
+def test_status_codes_before_launch(name, call, expected):
+    """Each entry point reports a bad call with its status code (LM_EINVAL 1,
+    LM_EUNSUPPORTED 2, LM_EWORKSPACE 4) before it launches anything, and
+    lm_status_string names it."""
+    handle = _lib.load()
+    assert call(handle) == expected, name
+    assert handle.lm_status_string(expected) != b"unknown status"
+
+
 def test_single_hip_runtime_in_process():
     import torch  # noqa: F401  (loads torch's HIP runtime)
     _lib.load()

@@ -269,6 +269,38 @@ def test_fused_experts_match_oracle(m, h, i, e, k):
     assert rel_l2(out, reference) < 2e-2          # the reference CPU path
 
 
+@pytest.mark.parametrize("m", [64, 600])
+@torch.inference_mode()
+def test_fused_experts_repeated_and_out_of_range_ids(m):
+    """Expert ids are device data and are not validated at the call. A token
+    that lists an expert several times gets every route computed and
+    combined (litemoe/ops.py:34-55 does the same); at m=64 (scan path) every
+    token lists expert 3 five times, so expert 3 has about 270 routes:
+    more than the call's 64 tokens and more than 256 (a per-expert route
+    list sized by the token count would drop the rest). Ids outside
+    [0, E) add nothing: compared with the oracle on the same routes with
+    those scales set to zero. m=600 takes the aligned-block path."""
+    h, i, e, k = 1536, 512, 40, 8
+    x, w1, w2, weights, ids = _moe_inputs(m, h, i, e, k, 300 + m)
+    ids = ids.clone()
+    ids[:, 3:] = 3                       # five repeats of expert 3 in every token
+    ids[::7] = 11                        # some tokens route all eight branches to 11
+    bad = torch.zeros_like(ids, dtype=torch.bool)
+    bad[1::5, 0] = True
+    bad[2::9, 2] = True
+    ids_dev = torch.where(bad, torch.where(torch.arange(m)[:, None] % 2 == 0, e, -1), ids)
+    out = experts.fused_experts(x.to(DEV), w1.to(DEV), w2.to(DEV), weights.to(DEV),
+                                ids_dev.int().to(DEV)).cpu()
+    scales = torch.where(bad, 0.0, weights)
+    safe_ids = torch.where(bad, 0, ids)
+    expected = ops.fused_moe(x, safe_ids.int(), scales, w1, w2)
+    assert rel_l2(out, expected) < 1e-2
+    reference = ops.reference_experts(x, safe_ids, scales.to(torch.bfloat16).float(), w1, w2, singleton=True)
+    assert rel_l2(out, reference) < 2e-2
+    per_row = (out.float() - expected.float()).norm(dim=1) / expected.float().norm(dim=1).clamp_min(1e-6)
+    assert float(per_row.max()) < 5e-2
+
+
 @torch.inference_mode()
 def test_fused_experts_block_rows_do_not_change_results():
     x, w1, w2, weights, ids = _moe_inputs(200, 1024, 512, 8, 2, 7)

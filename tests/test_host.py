@@ -138,3 +138,20 @@ def test_bench_refuses_multi_gpu():
     out = subprocess.run([sys.executable, "bench.py", "--gpus", "2"], capture_output=True, text=True,
                          cwd=str(__import__("pathlib").Path(__file__).resolve().parents[1]))
     assert out.returncode == 2 and "one GPU" in out.stderr
+
+
+def test_workspace_growth_keeps_handed_out_buffers():
+    """A captured graph keeps the address of the scratch it was given, so a
+    larger request must not release the earlier buffer (its storage stays
+    referenced and unchanged)."""
+    from litemoe_amd.experts import _Workspace
+    ws = _Workspace()
+    small = ws.get("cpu", 1000)
+    address = small.data_ptr()
+    assert ws.get("cpu", 800) is small  # fits: reused
+    large = ws.get("cpu", 5000)
+    assert large.numel() >= 5000 and large.data_ptr() != address
+    assert any(buf.data_ptr() == address for buf in ws.retired)
+    del small
+    assert any(buf.data_ptr() == address for buf in ws.retired)
+    assert ws.get("cpu", 5000) is large

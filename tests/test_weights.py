@@ -79,7 +79,11 @@ def test_saved_checkpoint_loads_the_hf_weights(tmp_path, shards, tied):
     assert_same_weights(bf, hf_weights(hf, torch.bfloat16))
 
 
-def test_reordering_placement_keeps_physical_order(tmp_path):
+def test_reordering_placement_fills_slots_by_inverse(tmp_path):
+    """``physical[layer][e]`` is the slot of expert e (litemoe/placement.py:31-38):
+    the router's id e is mapped to physical[e] before the GEMMs, so that slot
+    must hold expert e's weights. [2, 0, 3, 1] is not an involution, so
+    filling slot s with expert physical[s] instead would fail here."""
     hf = make_hf(seed=12)
     save_checkpoint(hf, tmp_path)
     cfg = W.load_config(tmp_path)
@@ -90,10 +94,15 @@ def test_reordering_placement_keeps_physical_order(tmp_path):
     for layer, order in enumerate(physical):
         g, e = got["layers"][layer], ref["layers"][layer]
         for name in ("input_linear", "output_linear"):
-            assert torch.equal(g[name], e[name][order]), name
+            for expert, slot in enumerate(order):
+                assert torch.equal(g[name][slot], e[name][expert]), (name, expert)
+            assert torch.equal(g[name], e[name][torch.tensor(order).argsort()]), name
         assert g["physical"].tolist() == order
         expect_logical = [] if order == sorted(order) else torch.tensor(order).argsort().tolist()
         assert g["logical"].tolist() == expect_logical
+        # the ids -> slot map and the combine's slot -> expert map are inverse
+        if expect_logical:
+            assert [expect_logical[slot] for slot in order] == list(range(len(order)))
     with pytest.raises(ValueError):
         W.load_weights(cfg, W.CheckpointSource(tmp_path), SimpleNamespace(world=2), 0, "cpu")
     bad = SimpleNamespace(world=1, physical=[[0, 0, 1, 2]] * 2, validate=lambda *a: None)
