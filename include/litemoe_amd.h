@@ -39,6 +39,13 @@ enum {
 const char *lm_version(void);
 const char *lm_status_string(int status);
 
+/* The device address of pinned host memory (hipHostMalloc'd, e.g. a torch
+ * tensor with pin_memory=True) for a kernel to write into: the emit ring of
+ * lm_greedy_epilogue. LM_EINVAL if the runtime does not know the pointer.
+ * Host-side helper of the output ring that replaces the reference's
+ * side-stream copies (litemoe/execution.py:25-41); it launches nothing. */
+int lm_host_device_pointer(void *host, void **device);
+
 /* ---------------------------------------------------------------- norms -- */
 
 /* y[r,:] = bf16( bf16(x[r,:] * rsqrt(mean(x[r,:]^2) + eps)) * w ), fp32 math.
@@ -401,13 +408,16 @@ int lm_moe_finish_add_rmsnorm(const void *y, const int32_t *ids,
  * (else LM_EUNSUPPORTED). row_order (int32 [rows], may be NULL): the rows
  * by descending used, equal used by ascending row (the stable argsort of
  * -used), for lm_flash_decode_qkv's dispatch order. No counterpart in the
- * reference, whose attention kernel schedules itself. */
+ * reference, whose attention kernel schedules itself. step_counter (int64
+ * [1] on the device, may be NULL) is incremented once per call: the step
+ * count lm_greedy_epilogue's emit ring is indexed by. */
 int lm_decode_prologue(const uint8_t *active, const int64_t *length,
                        const int64_t *next, const void *embedding,
                        float multiplier, const void *norm_weight, float eps,
                        void *x, void *z, uint8_t *valid, int64_t *positions,
-                       int32_t *used, int32_t *row_order, int64_t rows,
-                       int64_t hidden, int64_t vocab, void *stream);
+                       int32_t *used, int32_t *row_order,
+                       int64_t *step_counter, int64_t rows, int64_t hidden,
+                       int64_t vocab, void *stream);
 
 /* The end of one greedy decode step, per row b (one launch):
  *   candidate = argmax_v bf16(logits[b][v] * (1 / logits_scaling)), the
@@ -419,13 +429,20 @@ int lm_decode_prologue(const uint8_t *active, const int64_t *length,
  *   active[b] = valid[b] && !done.
  * Replaces litemoe/model.py:127 (/ logits_scaling) and engine.py:92-102.
  * logits: bf16 [rows][ld] raw head output; emit int64 [rows][3]; eos int64
- * [neos]. */
+ * [neos].
+ * emit_ring (may be NULL): the device address (lm_host_device_pointer) of
+ * int64 [ring_depth][rows][3] pinned host memory; each emit row is also
+ * stored, with system-scope stores, into slot (*step_counter - 1) %
+ * ring_depth, step_counter being the device counter lm_decode_prologue
+ * increments. This folds the per-step device-to-host copy of the
+ * reference's OutputRing (litemoe/execution.py:25-41) into the step. */
 int lm_greedy_epilogue(const void *logits, int64_t ld, float logits_scaling,
                        int64_t vocab, int64_t rows, const uint8_t *valid,
                        int64_t *next, int64_t *length, int64_t *generated,
                        const int64_t *budget, uint8_t *active, int64_t *emit,
                        const int64_t *eos, int64_t neos, int ignore_eos,
-                       void *stream);
+                       int64_t *emit_ring, int64_t ring_depth,
+                       const int64_t *step_counter, void *stream);
 
 #ifdef __cplusplus
 }

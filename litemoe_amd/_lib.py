@@ -52,9 +52,11 @@ _SIGNATURES = {
                             _f32, _i64, _i64, _v, _v, _i64, _v],
     "lm_add_rmsnorm_router_splitk": [_v, _v, _i64, _f32, _v, _f32, _v, _v, _i64, _i64, _i64, _i64,
                                      _i32, _v, _v, _v, _v],
-    "lm_decode_prologue": [_v, _v, _v, _v, _f32, _v, _f32, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _v],
-    "lm_greedy_epilogue": [_v, _i64, _f32, _i64, _i64, _v, _v, _v, _v, _v, _v, _v, _v, _i64, _i32,
+    "lm_decode_prologue": [_v, _v, _v, _v, _f32, _v, _f32, _v, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64,
                            _v],
+    "lm_greedy_epilogue": [_v, _i64, _f32, _i64, _i64, _v, _v, _v, _v, _v, _v, _v, _v, _i64, _i32,
+                           _v, _i64, _v, _v],
+    "lm_host_device_pointer": [_v, C.POINTER(C.c_void_p)],
 }
 _RESTYPE = {"lm_version": C.c_char_p, "lm_status_string": C.c_char_p}
 

@@ -1,4 +1,7 @@
-// Version and status strings of the C ABI.
+// Version and status strings of the C ABI, and the device address of pinned
+// host memory.
+#include <hip/hip_runtime.h>
+
 #include "../../include/litemoe_amd.h"
 
 extern "C" const char *lm_version(void) { return "litemoe_amd 0.1.0 gfx950"; }
@@ -12,4 +15,10 @@ extern "C" const char *lm_status_string(int status) {
     case LM_EWORKSPACE: return "workspace too small";
     default: return "unknown status";
   }
+}
+
+extern "C" int lm_host_device_pointer(void *host, void **device) {
+  if (!host || !device) return LM_EINVAL;
+  *device = nullptr;
+  return hipHostGetDevicePointer(device, host, 0) == hipSuccess ? LM_OK : LM_EINVAL;
 }

@@ -8,6 +8,14 @@
 //             tensor by a Python scalar as a product with the fp32
 //             reciprocal, so the epilogue does the same.
 //
+// Emit ring: with a step counter the prologue counts the step (one thread
+// adds 1) and the epilogue also stores each emit row into slot
+// (counter - 1) % depth of a ring in pinned host memory, with system-scope
+// stores that go straight to host memory. The decode step then publishes
+// its emit rows itself, inside the captured graph: the host reads a slot
+// after an event recorded behind the step, with no copy or stream of its
+// own.
+//
 // Reference: litemoe/engine.py:87-102 (decode_step), litemoe/model.py:103
 // (used), :104 (embedding * multiplier), :106 (first norm) and :127
 // (logits / logits_scaling).
@@ -27,7 +35,8 @@ prologue_kernel(const uint8_t *__restrict__ active, const int64_t *__restrict__ 
                 const bf16 *__restrict__ nw, float eps, bf16 *__restrict__ x,
                 bf16 *__restrict__ z, uint8_t *__restrict__ valid,
                 int64_t *__restrict__ positions, int32_t *__restrict__ used,
-                int32_t *__restrict__ order, int hidden, int64_t vocab) {
+                int32_t *__restrict__ order, int64_t *__restrict__ step_counter, int hidden,
+                int64_t vocab) {
   __shared__ float red[kThreads / kWave];
   __shared__ float rank_red[kThreads / kWave];
   const int64_t row = blockIdx.x;
@@ -47,6 +56,7 @@ prologue_kernel(const uint8_t *__restrict__ active, const int64_t *__restrict__ 
     valid[row] = act;
     positions[row] = pos;
     used[row] = (int32_t)(pos + 1);
+    if (step_counter && row == 0) *step_counter += 1;  // no other thread of the grid touches it
   }
   if (order) {
     // This row's rank among all rows by descending used (equal used: lower
@@ -127,7 +137,8 @@ epilogue_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, 
                 int64_t *__restrict__ length, int64_t *__restrict__ generated,
                 const int64_t *__restrict__ budget, uint8_t *__restrict__ active,
                 int64_t *__restrict__ emit, const int64_t *__restrict__ eos, int neos,
-                int ignore_eos) {
+                int ignore_eos, int64_t *__restrict__ ring, int64_t depth,
+                const int64_t *__restrict__ step_counter) {
   __shared__ float sv[kArgThreads / kWave];
   __shared__ int si[kArgThreads / kWave];
   const int64_t row = blockIdx.x;
@@ -217,6 +228,13 @@ epilogue_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, 
     emit[row * 3 + 0] = candidate;
     emit[row * 3 + 1] = gen;
     emit[row * 3 + 2] = val;
+    if (ring) {
+      const int64_t slot = ((*step_counter - 1) % depth + depth) % depth;
+      int64_t *dst = ring + (slot * (int64_t)gridDim.x + row) * 3;
+      __hip_atomic_store(dst + 0, candidate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(dst + 1, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(dst + 2, (int64_t)val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     const int64_t gen1 = gen + (val ? 1 : 0);
     length[row] = len + (val ? 1 : 0);
     generated[row] = gen1;
@@ -238,8 +256,8 @@ using namespace lm;
 extern "C" int lm_decode_prologue(const uint8_t *active, const int64_t *length, const int64_t *next,
                                   const void *embedding, float multiplier, const void *norm_weight,
                                   float eps, void *x, void *z, uint8_t *valid, int64_t *positions,
-                                  int32_t *used, int32_t *row_order, int64_t rows, int64_t hidden,
-                                  int64_t vocab, void *stream) {
+                                  int32_t *used, int32_t *row_order, int64_t *step_counter,
+                                  int64_t rows, int64_t hidden, int64_t vocab, void *stream) {
   LM_REQUIRE(rows >= 0 && hidden > 0 && vocab > 0);
   if (hidden % 8 || hidden > kMaxVec * 8 * kThreads) return LM_EUNSUPPORTED;
   if (rows == 0) return LM_OK;
@@ -247,7 +265,7 @@ extern "C" int lm_decode_prologue(const uint8_t *active, const int64_t *length, 
              positions && used);
   prologue_kernel<<<dim3((unsigned)rows), kThreads, 0, (hipStream_t)stream>>>(
       active, length, next, (const bf16 *)embedding, multiplier, (const bf16 *)norm_weight, eps,
-      (bf16 *)x, (bf16 *)z, valid, positions, used, row_order, (int)hidden, vocab);
+      (bf16 *)x, (bf16 *)z, valid, positions, used, row_order, step_counter, (int)hidden, vocab);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }
@@ -257,16 +275,17 @@ extern "C" int lm_greedy_epilogue(const void *logits, int64_t ld, float logits_s
                                   int64_t *next, int64_t *length, int64_t *generated,
                                   const int64_t *budget, uint8_t *active, int64_t *emit,
                                   const int64_t *eos, int64_t neos, int ignore_eos,
-                                  void *stream) {
+                                  int64_t *emit_ring, int64_t ring_depth,
+                                  const int64_t *step_counter, void *stream) {
   LM_REQUIRE(rows >= 0 && vocab > 0 && vocab < ((int64_t)1 << 31) && ld >= vocab && neos >= 0 &&
-             logits_scaling > 0.f);
+             logits_scaling > 0.f && (!emit_ring || (ring_depth > 0 && step_counter)));
   if (rows == 0) return LM_OK;
   LM_REQUIRE(logits && valid && next && length && generated && budget && active && emit &&
              (neos == 0 || eos));
   const float inv_scaling = 1.0f / logits_scaling;
   epilogue_kernel<<<dim3((unsigned)rows), kArgThreads, 0, (hipStream_t)stream>>>(
       (const bf16 *)logits, ld, inv_scaling, (int)vocab, valid, next, length, generated,
-      budget, active, emit, eos, (int)neos, ignore_eos);
+      budget, active, emit, eos, (int)neos, ignore_eos, emit_ring, ring_depth, step_counter);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

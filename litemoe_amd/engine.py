@@ -1,11 +1,24 @@
-"""Requests, GPU-owned greedy state, the decode step and the generate loop.
+"""Requests, the GPU-resident greedy state, the decode step and the generate loop.
 
-Mirrors litemoe/engine.py:15-221 for one GPU: the same state tensors
-(``next``, ``length``, ``generated``, ``budget``, ``present``, ``active``),
-the same ``emit [B, 3] = (token, index, valid)`` snapshot, the same capacity
-rule and metrics (``decode_tps = decode_tokens / decode_s``). Prefill is the
-packed ragged path (litemoe/packed.py:19-36), run in chunks of at most
-``prefill_tokens`` tokens.
+The public surface is the reference's (litemoe/engine.py:15-221): ``Request``,
+``Engine(model, requests, world, rank, mode, ignore_eos, poll, capacity,
+host_process)``, ``decode_step()``, ``prefill()``, ``prepare_graph()``,
+``stopped()`` and ``generate()`` with the same metrics keys, the same
+``emit [B, 3] = (token, index, valid)`` snapshot and its ordering check.
+The engine runs one GPU (world 1). What differs is how a step runs:
+
+* the decode step's set-up and its argmax/state update are one kernel each
+  (``lm_decode_prologue``, ``lm_greedy_epilogue``) around the layers; a step
+  on a model without that path runs its forward and then the same epilogue
+  kernel, so both share one state update;
+* in ``graph-async`` mode the epilogue also writes each step's emit rows
+  straight into a pinned host ring (:class:`OutputRing`), so a replay is the
+  only launch per step;
+* when to stop is read from the delivered snapshots (a row ends when its
+  outputs reach its budget or its last token is a stop id), so the loop
+  polls without a device synchronisation;
+* prefill is packed and ragged (litemoe/packed.py:19-36), in chunks of at
+  most ``prefill_tokens`` tokens.
 """
 import math
 import time
@@ -16,6 +29,11 @@ import torch
 from .cache import KVCache
 from .execution import OutputRing, capture_decode
 from .packed import packed_prefill_logits
+from .step import greedy_epilogue
+
+CONTEXT_LIMIT = 4096
+STATE_FIELDS = (("next", torch.int64), ("length", torch.int64), ("generated", torch.int64),
+                ("budget", torch.int64), ("present", torch.bool), ("active", torch.bool))
 
 
 @dataclass
@@ -25,101 +43,117 @@ class Request:
     budget: int
 
 
-def prepare_batch(model, tokens):
-    """Grow the expert dispatch capacity for ``tokens`` rows (batch.py:7-11)."""
-    model.ep.capacity = max(model.ep.capacity, tokens)
-    model.ep.prepare(tokens)
+@dataclass
+class _Plan:
+    """Validated requests of one engine and the KV capacity they need."""
+    live: list
+    empty: dict
+    capacity: int
+
+
+def plan_requests(requests, cfg, mode, capacity, rope_rows):
+    """Check a request list the way litemoe/engine.py:33-51 does (same
+    messages) and choose the KV capacity: the longest prompt plus its budget,
+    rounded up to a power of two for the graph modes."""
+    if any(type(r.budget) is not int or r.budget < 0 for r in requests):
+        raise ValueError("Output budgets must be nonnegative integers")
+    if len({r.request_id for r in requests}) != len(requests):
+        raise ValueError("Request ids must be unique")
+    live = [r for r in requests if r.budget]
+    empty = {r.request_id: [] for r in requests if not r.budget}
+    vocab = cfg.vocab_size
+    for r in live:
+        if not r.prompt or any(type(t) is not int or not 0 <= t < vocab for t in r.prompt):
+            raise ValueError("Each prompt must contain valid vocabulary ids")
+    limit = min(CONTEXT_LIMIT, cfg.max_position_embeddings)
+    need = max((len(r.prompt) + r.budget - 1 for r in live), default=1)
+    if need > limit:
+        raise ValueError("Request exceeds the model context limit")
+    if capacity is None:
+        capacity = need if mode == "eager" else 1 << math.ceil(math.log2(need))
+    if not need <= capacity <= limit:
+        raise ValueError("Insufficient/unsupported KV capacity")
+    if capacity > rope_rows:
+        raise ValueError("KV capacity exceeds the model's RoPE table")
+    return _Plan(live, empty, capacity)
 
 
 class Engine:
     cache_type = KVCache
     prefill_tokens = 1 << 17
+    ring_depth = 4
 
     def __init__(self, model, requests, world=1, rank=0, mode="eager", ignore_eos=False, poll=1,
                  capacity=None, host_process=None):
         if world != 1 or rank != 0:
             raise ValueError("This build runs one engine per GPU (world == 1)")
-        self.model, self.world, self.rank = model, world, rank
-        self.device, self.dtype = model.w["embedding"].device, model.w["embedding"].dtype
         if poll < 1 or mode not in ("eager", "graph", "graph-async"):
             raise ValueError("Invalid execution mode or polling period")
-        if any(type(r.budget) is not int or r.budget < 0 for r in requests):
-            raise ValueError("Output budgets must be nonnegative integers")
-        if len({r.request_id for r in requests}) != len(requests):
-            raise ValueError("Request ids must be unique")
-        self.empty = {r.request_id: [] for r in requests if r.budget == 0}
-        self.requests = [r for r in requests if r.budget]
-        cfg = model.cfg
-        if any(not r.prompt or any(type(t) is not int or not 0 <= t < cfg.vocab_size for t in r.prompt)
-               for r in self.requests):
-            raise ValueError("Each prompt must contain valid vocabulary ids")
-        required = max((len(r.prompt) + r.budget - 1 for r in self.requests), default=1)
-        if required > min(4096, cfg.max_position_embeddings):
-            raise ValueError("Request exceeds the model context limit")
-        cap = capacity or (2 ** math.ceil(math.log2(required)) if mode != "eager" else required)
-        if cap < required or cap > min(4096, cfg.max_position_embeddings):
-            raise ValueError("Insufficient/unsupported KV capacity")
-        if cap > model.capacity:
-            raise ValueError("KV capacity exceeds the model's RoPE table")
-        self.capacity = cap
-        self.batch = len(self.requests)
+        self.model, self.world, self.rank = model, world, rank
+        embedding = model.w["embedding"]
+        self.device, self.dtype = embedding.device, embedding.dtype
+        plan = plan_requests(requests, model.cfg, mode, capacity, model.capacity)
+        self.requests, self.empty, self.capacity = plan.live, plan.empty, plan.capacity
         self.local = self.requests
-        self.mode, self.ignore_eos, self.poll = mode, ignore_eos, poll
-        self.host_process = host_process
+        self.batch = len(self.requests)
+        self.mode, self.ignore_eos, self.poll, self.host_process = mode, ignore_eos, poll, host_process
         self.graph = None
+        self.ring = None
         if not self.requests:
             return
         if self.device.type != "cuda":
             raise ValueError("This engine runs on the GPU path only")
         if mode != "eager" and not model.ep.backend.graph_safe:
             raise ValueError("Full Decode Graph requires a graph-safe expert backend")
-        self.cache = self.cache_type(cfg, self.batch, cap, self.device, self.dtype)
-        self.state = {name: torch.zeros(self.batch, dtype=dtype, device=self.device) for name, dtype in (
-            ("next", torch.int64), ("length", torch.int64), ("generated", torch.int64),
-            ("budget", torch.int64), ("present", torch.bool), ("active", torch.bool),
-        )}
+        cfg = model.cfg
+        self.cache = self.cache_type(cfg, self.batch, self.capacity, self.device, self.dtype)
+        self.state = {name: torch.zeros(self.batch, dtype=dtype, device=self.device)
+                      for name, dtype in STATE_FIELDS}
         self.emit = torch.zeros(self.batch, 3, dtype=torch.int64, device=self.device)
         eos = cfg.eos_token_id
-        self.eos = torch.tensor(eos if isinstance(eos, list) else ([] if eos is None else [eos]),
-                                device=self.device, dtype=torch.int64)
-        prepare_batch(model, self.batch)
+        self.eos_ids = [] if eos is None else list(eos) if isinstance(eos, (list, tuple)) else [eos]
+        self.eos = torch.tensor(self.eos_ids, device=self.device, dtype=torch.int64)
+        self.budgets = [r.budget for r in self.requests]
+        self._consumer = None
+        self.ring = OutputRing(self.emit, self._consume, mode == "graph-async", self.ring_depth)
+        model.ep.capacity = max(model.ep.capacity, self.batch)
+        model.ep.prepare(self.batch)
         self.reset()
 
+    # -- state ---------------------------------------------------------------
     def reset(self):
         self.cache.reset()
-        for value in self.state.values():
+        s = self.state
+        for value in s.values():
             value.zero_()
-        budgets = torch.tensor([r.budget for r in self.local], dtype=torch.int64)
-        self.state["budget"].copy_(budgets)
-        self.state["present"].fill_(True)
+        s["budget"].copy_(torch.tensor(self.budgets, dtype=torch.int64))
+        s["present"].fill_(True)
         self.emit.zero_()
 
     def is_eos(self, token):
-        if self.eos.numel() == 0:
+        if not self.eos_ids:
             return torch.zeros_like(token, dtype=torch.bool)
-        return (token[:, None] == self.eos[None, :]).any(-1)
+        return torch.isin(token, self.eos)
 
+    def stopped(self):
+        """Whether no row is active (reads the device state; the generate
+        loop decides from the delivered snapshots instead)."""
+        return not bool(self.state["active"].any())
+
+    # -- one decode step ---------------------------------------------------------
     def decode_step(self):
         s = self.state
+        ring = self.ring if self.ring is not None and self.ring.asynchronous else None
         if getattr(self.model, "decode_lean", False) and self.model.greedy_supported():
-            # Lean decode: the step's set-up and its argmax/state update run
-            # as one kernel each around the layers (same tokens and state).
-            self.model.greedy_step(s, self.emit, self.eos, self.ignore_eos, self.cache)
+            self.model.greedy_step(s, self.emit, self.eos, self.ignore_eos, self.cache, ring=ring)
             return
+        # Any other model: the torch prologue, its forward (which divides by
+        # logits_scaling itself, so the epilogue scales by 1: an exact
+        # product), and the shared epilogue kernel for argmax and state.
         valid = s["active"].clone()
         positions = torch.where(valid, s["length"], 0)[:, None]
-        logits = self.model.forward(s["next"][:, None], positions, valid[:, None], self.cache)
-        candidate = logits[:, 0].argmax(-1)
-        self.emit[:, 0].copy_(candidate)
-        self.emit[:, 1].copy_(s["generated"])
-        self.emit[:, 2].copy_(valid)
-        s["length"].add_(valid)
-        s["generated"].add_(valid)
-        s["next"].copy_(torch.where(valid, candidate, s["next"]))
-        done = s["generated"] >= s["budget"]
-        if not self.ignore_eos:
-            done = done | self.is_eos(candidate)
-        s["active"].copy_(valid & ~done)
+        logits = self.model.forward(s["next"][:, None], positions, valid[:, None], self.cache)[:, 0]
+        greedy_epilogue(logits, 1.0, valid, s, self.emit, self.eos, self.ignore_eos)
 
     def prepare_graph(self):
         if self.mode == "eager" or self.graph is not None or not self.requests:
@@ -127,43 +161,49 @@ class Engine:
         if self.model.trace is not None:
             raise ValueError("Trace/count collection must be disabled during capture/timing")
 
-        def warm_state():
+        def steady():  # every present row active, one token of budget left
             self.reset()
             self.state["active"].copy_(self.state["present"])
             self.state["budget"].fill_(2)
 
-        self.graph = capture_decode(self.decode_step, warm_state)
+        self.graph = capture_decode(self.decode_step, steady)
         self.reset()
 
     def synchronize(self):
         torch.cuda.synchronize(self.device)
 
-    def stopped(self):
-        return self.state["active"].sum(dtype=torch.int64).item() == 0
-
+    # -- prefill -------------------------------------------------------------------
     def prefill_logits(self, prompts):
         """Last-position logits of every prompt, packed in token-bounded chunks."""
-        out, start = [], 0
+        chunks, start = [], 0
         while start < len(prompts):
-            end, tokens = start, 0
-            while end < len(prompts) and (end == start or tokens + len(prompts[end]) <= self.prefill_tokens):
+            end, tokens = start + 1, len(prompts[start])
+            while end < len(prompts) and tokens + len(prompts[end]) <= self.prefill_tokens:
                 tokens += len(prompts[end])
                 end += 1
-            prepare_batch(self.model, tokens)
-            out.append(packed_prefill_logits(self.model, prompts[start:end], self.cache, start))
+            self.model.ep.capacity = max(self.model.ep.capacity, tokens)
+            self.model.ep.prepare(tokens)
+            chunks.append(packed_prefill_logits(self.model, prompts[start:end], self.cache, start))
             start = end
-        return out[0] if len(out) == 1 else torch.cat(out)
+        return chunks[0] if len(chunks) == 1 else torch.cat(chunks)
 
     def prefill(self):
+        """Prefill every request and set the state for the first decode step:
+        the first token, lengths, one output generated, and the row active
+        unless its budget is 1 or (without ignore_eos) the token stops it."""
         first = self.prefill_logits([r.prompt for r in self.local])[:, 0].argmax(-1)
         s = self.state
         s["next"].copy_(first)
         s["length"].copy_(torch.tensor([len(r.prompt) for r in self.local], device=self.device))
         s["generated"].copy_(s["present"])
-        active = s["present"] & (s["budget"] > 1)
+        keep = s["present"] & (s["budget"] > 1)
         if not self.ignore_eos:
-            active &= ~self.is_eos(first)
-        s["active"].copy_(active)
+            keep &= ~self.is_eos(first)
+        s["active"].copy_(keep)
+
+    # -- generation ------------------------------------------------------------------
+    def _consume(self, rows):
+        self._consumer(rows)
 
     @torch.inference_mode()
     def generate(self, step_events=None):
@@ -173,17 +213,23 @@ class Engine:
         self.prepare_graph()
         self.reset()
         outputs = [[] for _ in self.local]
+        open_rows = set(range(self.batch))  # rows whose snapshots may still add tokens
+        stops = set(self.eos_ids)
 
         def consume(rows):
             for slot, (token, index, valid) in enumerate(rows):
-                if valid:
-                    if slot >= len(outputs) or index != len(outputs[slot]):
-                        raise RuntimeError("Lost, duplicated or reordered output snapshot")
-                    outputs[slot].append(token)
-                    if self.host_process:
-                        self.host_process(outputs[slot])
+                if not valid:
+                    continue
+                out = outputs[slot] if slot < len(outputs) else None
+                if out is None or index != len(out):
+                    raise RuntimeError("Lost, duplicated or reordered output snapshot")
+                out.append(token)
+                if self.host_process:
+                    self.host_process(out)
+                if len(out) >= self.budgets[slot] or (not self.ignore_eos and token in stops):
+                    open_rows.discard(slot)
 
-        ring = OutputRing(self.emit, consume, self.mode == "graph-async")
+        self._consumer = consume
         self.synchronize()
         start = time.perf_counter()
         self.prefill()
@@ -191,36 +237,35 @@ class Engine:
         self.emit[:, 0].copy_(s["next"])
         self.emit[:, 1].zero_()
         self.emit[:, 2].copy_(s["present"])
-        consume(self.emit.cpu().tolist())  # first tokens are published before decode
+        consume(self.emit.cpu().tolist())  # the first tokens, before any decode step
         self.synchronize()
         prefill_end = time.perf_counter()
-        hard_limit = max(r.budget for r in self.requests) - 1
-        done = not self.ignore_eos and self.stopped()
-        for n in range(hard_limit):
-            if done:
+        self.ring.start()
+        steps = max(self.budgets) - 1
+        for n in range(steps):
+            if not self.ignore_eos and n % self.poll == 0 and not open_rows:
                 break
             if step_events is not None:
                 begin, finish = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 begin.record()
-            if self.graph:
+            if self.graph is not None:
                 self.graph.replay()
             else:
                 self.decode_step()
             if step_events is not None:
                 finish.record()
                 step_events.append((begin, finish))
-            ring.publish(n)
-            if not self.ignore_eos and (n + 1) % self.poll == 0:
-                done = self.stopped()
-        ring.drain()
+            self.ring.publish(n)
+        self.ring.drain()
         self.synchronize()
         end = time.perf_counter()
-        p, d, e = prefill_end - start, end - prefill_end, end - start
-        inp = sum(len(r.prompt) for r in self.local)
-        out = sum(map(len, outputs))
-        dec = sum(max(len(o) - 1, 0) for o in outputs)
+        prefill_s, decode_s, e2e_s = prefill_end - start, end - prefill_end, end - start
+        input_tokens = sum(len(r.prompt) for r in self.local)
+        output_tokens = sum(map(len, outputs))
+        decode_tokens = sum(max(len(o) - 1, 0) for o in outputs)
         result = {r.request_id: o for r, o in zip(self.local, outputs)}
         result.update(self.empty)
-        return result, dict(prefill_s=p, decode_s=d, e2e_s=e, input_tokens=inp, output_tokens=out,
-                            decode_tokens=dec, decode_tps=dec / d if dec else None, e2e_tps=out / e,
-                            capacity=self.capacity)
+        return result, dict(prefill_s=prefill_s, decode_s=decode_s, e2e_s=e2e_s, input_tokens=input_tokens,
+                            output_tokens=output_tokens, decode_tokens=decode_tokens,
+                            decode_tps=decode_tokens / decode_s if decode_tokens else None,
+                            e2e_tps=output_tokens / e2e_s, capacity=self.capacity)

@@ -1,70 +1,139 @@
-"""HIP-graph capture of one decode step and a race-free device->host ring.
+"""The decode step as a HIP graph, and the emit ring of the generate loop.
 
-Mirrors litemoe/execution.py:6-64 on ROCm: ``torch.cuda.CUDAGraph`` records a
-hipGraph, ``OutputRing`` double-buffers the per-step emit tensor into pinned
-host memory on a side stream (default priority) with events, so the host
-never blocks the next replay.
+``capture_decode(step, reset)`` returns a :class:`StepGraph`: one decode
+step recorded by stream capture, replayed with one launch per step
+(litemoe/execution.py:48-64 is the reference's counterpart).
+
+``OutputRing(emit, consume, asynchronous=False, depth=4)`` hands the
+per-step snapshots of ``emit [B, 3] = (token, index, valid)`` to
+``consume`` in step order, each exactly once (litemoe/execution.py:6-45 is
+the reference's counterpart; its contract is kept, its mechanism is not):
+
+* synchronous: a blocking copy after every step;
+* asynchronous: ``depth`` slots of pinned host memory. A slot is filled in
+  one of two ways. With a device view (:meth:`OutputRing.device_target`)
+  the step's greedy epilogue kernel stores the rows into the slot itself,
+  so the device-to-host transfer is part of the captured step and needs no
+  copy, stream or cross-stream wait of its own; otherwise a copy is queued
+  behind the step on the compute stream. Either way an event recorded
+  behind step n tells when slot ``n % depth`` holds step n. Slot reuse is
+  safe because ``publish(n)`` consumes step ``n + 1 - depth`` before it
+  returns, i.e. before the step that writes that slot again is queued; the
+  host runs at most ``depth - 1`` steps ahead of the device.
 """
+import ctypes
+from collections import deque
+
 import torch
 
-
-class OutputRing:
-    def __init__(self, emit, consume, asynchronous=False):
-        self.emit, self.consume = emit, consume
-        self.asynchronous = asynchronous
-        self.pending = [False, False]
-        self.used = [False, False]
-        if asynchronous:
-            self.device = [torch.empty_like(emit) for _ in range(2)]
-            self.host = [torch.empty(emit.shape, dtype=emit.dtype, pin_memory=True) for _ in range(2)]
-            self.ready = [torch.cuda.Event() for _ in range(2)]
-            self.copied = [torch.cuda.Event() for _ in range(2)]
-            self.stream = torch.cuda.Stream(device=emit.device)
-
-    def take(self, s):
-        if self.pending[s]:
-            self.copied[s].synchronize()
-            self.consume(self.host[s].tolist())
-            self.pending[s] = False
-
-    def publish(self, n):
-        if not self.asynchronous:
-            self.consume(self.emit.cpu().tolist())
-            return
-        s = n % 2
-        self.take(s)
-        compute = torch.cuda.current_stream(self.emit.device)
-        if self.used[s]:
-            compute.wait_event(self.copied[s])
-        self.device[s].copy_(self.emit)
-        self.ready[s].record(compute)
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(self.ready[s])
-            self.host[s].copy_(self.device[s], non_blocking=True)
-            self.copied[s].record()
-        self.pending[s] = self.used[s] = True
-        self.take((n - 1) % 2)
-
-    def drain(self):
-        for s in range(2):
-            self.take(s)
+from . import _lib
 
 
-def capture_decode(step, reset, warmups=3):
-    """Warm the step on a side stream, then record it into a hipGraph.
-    Warm-up and capture mutate state; the caller restores it (execution.py:48-64)."""
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
+class StepGraph:
+    """One recorded decode step; :meth:`replay` launches it on the current stream."""
+
+    def __init__(self, graph, stream, pool):
+        self.graph, self.stream, self.pool = graph, stream, pool
+
+    def replay(self):
+        self.graph.replay()
+
+
+def capture_decode(step, reset, warmups=2, pool=None):
+    """Record ``step`` into a HIP graph.
+
+    ``step`` runs ``warmups`` times first, each after ``reset``, on the
+    capture stream, so that lazy set-up (library handles, workspaces, cached
+    buffers) happens outside the recording; the recording itself also
+    advances the state, so ``reset`` runs once more before returning. A
+    ``pool`` (``torch.cuda.graph_pool_handle()``) lets several step graphs
+    share their private memory. Stream priorities stay at the default."""
+    if warmups < 1:
+        raise ValueError("capture needs at least one warm-up step")
+    caller = torch.cuda.current_stream()
+    stream = torch.cuda.Stream(device=caller.device)
+    stream.wait_stream(caller)
+    graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         for _ in range(warmups):
             reset()
             step()
         reset()
-    torch.cuda.current_stream().wait_stream(stream)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        step()
-    torch.cuda.synchronize()
+        stream.synchronize()
+        with torch.cuda.graph(graph, pool=pool, stream=stream):
+            step()
+    caller.wait_stream(stream)
     reset()
-    return graph
+    torch.cuda.synchronize(caller.device)
+    return StepGraph(graph, stream, graph.pool() if pool is None else pool)
+
+
+class OutputRing:
+    """Ordered, exactly-once delivery of the per-step emit snapshots."""
+
+    def __init__(self, emit, consume, asynchronous=False, depth=4):
+        if depth < 2:
+            raise ValueError("an asynchronous ring needs at least two slots")
+        self.emit, self.consume = emit, consume
+        self.asynchronous = asynchronous
+        self.depth = depth
+        self.pending = deque()        # published steps not yet consumed, ascending
+        self.device_writes = False    # set once a step's epilogue writes the slots
+        self._device_ptr = None
+        self.counter = None
+        if asynchronous:
+            self.host = torch.empty((depth, *emit.shape), dtype=emit.dtype, pin_memory=True)
+            self.events = [torch.cuda.Event() for _ in range(depth)]
+
+    # -- device view -----------------------------------------------------
+    def device_target(self, rows):
+        """``(device address of the slots, depth, step counter)`` for the
+        greedy epilogue to write into, and the counter the decode prologue
+        increments. After this call :meth:`publish` copies nothing."""
+        if not self.asynchronous:
+            raise ValueError("only an asynchronous ring has host slots to write")
+        if rows != self.emit.shape[0]:
+            raise ValueError("emit rows do not match the ring")
+        if self._device_ptr is None:
+            address = ctypes.c_void_p()
+            _lib.call("lm_host_device_pointer", self.host.data_ptr(), ctypes.byref(address))
+            self._device_ptr = address.value
+            self.counter = torch.zeros(1, dtype=torch.int64, device=self.emit.device)
+        self.device_writes = True
+        return self._device_ptr, self.depth, self.counter
+
+    def start(self):
+        """Begin a run of steps numbered from 0 (clears the step counter;
+        captured warm-ups advance it too)."""
+        if self.pending:
+            raise RuntimeError("start() with snapshots still pending")
+        if self.counter is not None:
+            self.counter.zero_()
+
+    # -- delivery ----------------------------------------------------------
+    def _deliver(self, n):
+        slot = n % self.depth
+        self.events[slot].synchronize()
+        self.consume(self.host[slot].tolist())
+
+    def publish(self, n):
+        """Step ``n`` (0, 1, 2, ... in order) has been queued."""
+        if not self.asynchronous:
+            self.consume(self.emit.cpu().tolist())
+            return
+        if self.pending and n != self.pending[-1] + 1:
+            raise RuntimeError("steps must be published in order")
+        slot = n % self.depth
+        if not self.device_writes:
+            self.host[slot].copy_(self.emit, non_blocking=True)
+        self.events[slot].record()
+        self.pending.append(n)
+        # Step n + 1 writes slot (n + 1) % depth: deliver its previous
+        # occupant now, then whatever else has already landed.
+        while self.pending and (self.pending[0] <= n + 1 - self.depth
+                                or self.events[self.pending[0] % self.depth].query()):
+            self._deliver(self.pending.popleft())
+
+    def drain(self):
+        while self.pending:
+            self._deliver(self.pending.popleft())

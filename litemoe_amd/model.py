@@ -164,21 +164,25 @@ class Granite:
         h = self.cfg.hidden_size
         return bool(self.decode_lean) and self._fused_moe() and h % 8 == 0 and h <= 4096
 
-    def greedy_step(self, state, emit, eos, ignore_eos, cache):
+    def greedy_step(self, state, emit, eos, ignore_eos, cache, ring=None):
         """One lean greedy decode step from the engine's state to its update:
         prologue kernel (valid, positions, ``used``, embedding, first norm),
         the fused layers, the raw head product and the epilogue kernel
         (argmax of ``logits / logits_scaling``, emit row, state update).
         Same tokens and state as litemoe/engine.py:87-102 around this model's
-        forward (model.py:95-127) in lean decode."""
+        forward (model.py:95-127) in lean decode. With an asynchronous
+        ``ring`` the epilogue also stores the emit rows into the ring's slot
+        for this step (counted by the prologue)."""
         cfg = self.cfg
+        rows = state["active"].shape[0]
         order = getattr(self.decode_flash, "row_order", None)
-        if order is not None and order.shape[0] != state["active"].shape[0]:
+        if order is not None and order.shape[0] != rows:
             order = None
+        target = ring.device_target(rows) if ring is not None else None
         x, z, valid, positions, used = decode_prologue(
             state["active"], state["length"], state["next"], self.w["embedding"],
             cfg.embedding_multiplier, self.w["layers"][0]["input_layernorm"], cfg.rms_norm_eps,
-            row_order=order)
+            row_order=order, step_counter=None if target is None else target[2])
         self.used = used
         self._row_order = order  # valid for this step only: the prologue just wrote it
         try:
@@ -186,7 +190,7 @@ class Granite:
         finally:
             self._row_order = None
         greedy_epilogue(F.linear(z, self.w["head"]), cfg.logits_scaling, valid, state, emit, eos,
-                        ignore_eos)
+                        ignore_eos, ring_target=target)
 
     def forward(self, tokens, positions, valid, cache, slot=None, last=None, communication_tokens=None):
         cfg = self.cfg

@@ -19,14 +19,16 @@ def _bool_bytes(t):
     return t.view(torch.uint8)
 
 
-def decode_prologue(active, length, next_tokens, embedding, multiplier, norm_weight, eps, row_order=None):
+def decode_prologue(active, length, next_tokens, embedding, multiplier, norm_weight, eps, row_order=None,
+                    step_counter=None):
     """Returns ``(x, z, valid, positions, used)`` for one decode step.
 
     ``valid = active``; ``positions = where(valid, length, 0)``;
     ``used = int32(positions + 1)``; ``x = embedding[next] * multiplier``
     (bf16); ``z = rmsnorm(x, norm_weight, eps)``. With ``row_order`` (int32
     ``[rows]``) also the rows by descending ``used`` (ties by row), the
-    dispatch order for :meth:`FlashDecode.fused_qkv`.
+    dispatch order for :meth:`FlashDecode.fused_qkv`. ``step_counter``
+    (int64 ``[1]``) is incremented: the step count an emit ring is indexed by.
     """
     _lib.require_cuda(active, length, next_tokens, embedding, norm_weight, what="decode prologue inputs")
     rows = active.shape[0]
@@ -47,21 +49,26 @@ def decode_prologue(active, length, next_tokens, embedding, multiplier, norm_wei
     if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (rows,)
                                   or not row_order.is_contiguous()):
         raise ValueError("row_order must be a contiguous int32 [rows] tensor")
+    if step_counter is not None and (step_counter.dtype != torch.int64 or step_counter.numel() != 1):
+        raise ValueError("step_counter must be an int64 [1] tensor")
     _lib.call("lm_decode_prologue", _bool_bytes(active).data_ptr(), length.data_ptr(),
               next_tokens.data_ptr(), embedding.data_ptr(), float(multiplier), norm_weight.data_ptr(),
               float(eps), x.data_ptr(), z.data_ptr(), valid.view(torch.uint8).data_ptr(),
-              positions.data_ptr(), used.data_ptr(), _lib.ptr(row_order), rows, hidden, vocab,
-              _lib.stream(dev))
+              positions.data_ptr(), used.data_ptr(), _lib.ptr(row_order), _lib.ptr(step_counter), rows,
+              hidden, vocab, _lib.stream(dev))
     return x, z, valid, positions, used
 
 
-def greedy_epilogue(logits, logits_scaling, valid, state, emit, eos, ignore_eos):
+def greedy_epilogue(logits, logits_scaling, valid, state, emit, eos, ignore_eos, ring_target=None):
     """Greedy token choice and the engine's state update, in place.
 
     ``logits`` is the raw head output ``[rows, vocab]`` (before
     ``/ logits_scaling``); ``state`` holds the engine's ``next``,
     ``length``, ``generated``, ``budget`` (int64) and ``active`` (bool);
     ``emit`` is ``[rows, 3]`` int64; ``eos`` an int64 tensor of stop ids.
+    ``ring_target`` (``OutputRing.device_target(rows)``: the ring's device
+    address, depth and step counter) also receives the emit rows, in slot
+    ``(counter - 1) % depth``.
     """
     _lib.require_cuda(logits, valid, emit, eos, what="greedy epilogue inputs")
     rows, vocab = logits.shape
@@ -75,9 +82,10 @@ def greedy_epilogue(logits, logits_scaling, valid, state, emit, eos, ignore_eos)
         raise ValueError("emit must be contiguous int64 [rows, 3]")
     if eos.dtype != torch.int64 or not eos.is_contiguous():
         raise ValueError("eos must be a contiguous int64 tensor")
+    ring_ptr, depth, counter = (None, 0, None) if ring_target is None else ring_target
     _lib.call("lm_greedy_epilogue", logits.data_ptr(), logits.stride(0), float(logits_scaling), vocab,
               rows, _bool_bytes(valid).data_ptr(), state["next"].data_ptr(), state["length"].data_ptr(),
               state["generated"].data_ptr(), state["budget"].data_ptr(),
               _bool_bytes(state["active"]).data_ptr(), emit.data_ptr(),
               eos.data_ptr() if eos.numel() else None, eos.numel(), int(bool(ignore_eos)),
-              _lib.stream(logits.device))
+              ring_ptr, depth, _lib.ptr(counter), _lib.stream(logits.device))

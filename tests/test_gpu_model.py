@@ -200,15 +200,17 @@ def test_full_size_graph_replay_equals_eager(name, batch, lengths, capacity):
     eager_run = OptimizedEngine(model, requests, ignore_eos=True, capacity=capacity)
     eager, _ = eager_run.generate()
     assert all(len(t) == 5 and all(0 <= x < cfg.vocab_size for x in t) for t in eager.values())
-    graph_run = OptimizedEngine(model, requests, ignore_eos=True, capacity=capacity, mode="graph")
-    for _ in range(2):
-        actual, metrics = graph_run.generate()
-        assert actual == eager
-        assert metrics["output_tokens"] == batch * 5
-        for k in eager_run.state:
-            assert torch.equal(graph_run.state[k], eager_run.state[k]), k
-        assert torch.equal(graph_run.cache.k, eager_run.cache.k)
-        assert torch.equal(graph_run.cache.v, eager_run.cache.v)
-    del eager_run, graph_run, model, w
+    for mode in ("graph", "graph-async"):  # graph-async: the epilogue writes the pinned emit ring
+        graph_run = OptimizedEngine(model, requests, ignore_eos=True, capacity=capacity, mode=mode)
+        for _ in range(2):
+            actual, metrics = graph_run.generate()
+            assert actual == eager
+            assert metrics["output_tokens"] == batch * 5
+            for k in eager_run.state:
+                assert torch.equal(graph_run.state[k], eager_run.state[k]), k
+            assert torch.equal(graph_run.cache.k, eager_run.cache.k)
+            assert torch.equal(graph_run.cache.v, eager_run.cache.v)
+        del graph_run
+    del eager_run, model, w
     torch.cuda.empty_cache()
 
