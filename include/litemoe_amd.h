@@ -32,7 +32,8 @@ enum {
   LM_EINVAL = 1,        /* invalid argument (null pointer, negative size, bad shape) */
   LM_EUNSUPPORTED = 2,  /* shape this build has no kernel for (e.g. head_dim != 64) */
   LM_ELAUNCH = 3,       /* the HIP runtime rejected a kernel launch */
-  LM_EWORKSPACE = 4     /* workspace smaller than the size query returned */
+  LM_EWORKSPACE = 4,    /* workspace smaller than the size query returned */
+  LM_ETOOLARGE = 5      /* problem larger than lm_fused_experts_noalloc's static scratch */
 };
 
 /* Library version string and a message for a status code. */
@@ -262,6 +263,25 @@ int lm_fused_experts(const void *x, const void *w13, const void *w2,
                      int64_t inter, int64_t experts, int64_t topk,
                      int64_t block_rows, void *out, void *workspace,
                      int64_t workspace_bytes, void *stream);
+
+/* lm_fused_experts with no workspace argument and no allocation of any kind
+ * (no hipMalloc/hipFree, no allocating library call). No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Its
+ * scratch is a static device array of 16 MiB per GPU, held from the
+ * library's load until the process ends; a call whose workspace
+ * (lm_fused_experts_workspace_size) exceeds it returns LM_ETOOLARGE (the
+ * decode shapes fit: 64 tokens x top-8 at hidden 1536 needs about 2 MiB,
+ * 256 tokens about 8 MiB). stream must belong to the current device.
+ * Results are bitwise those of lm_fused_experts. All calls on one GPU share
+ * that GPU's array: calls that overlap on one GPU (two streams, or two host
+ * threads) race. */
+int lm_fused_experts_noalloc(const void *x, const void *w13, const void *w2,
+                             const float *topk_weights,
+                             const int32_t *topk_ids, const int64_t *logical,
+                             int64_t tokens, int64_t hidden, int64_t inter,
+                             int64_t experts, int64_t topk, int64_t block_rows,
+                             void *out, void *stream);
 
 /* Stage entry points of lm_fused_experts, exposed for parity tests and
  * kernel timing. For a route r = t*topk + j of expert e:

@@ -39,6 +39,7 @@ _SIGNATURES = {
     "lm_fused_experts_workspace_size": [_i64, _i64, _i64, _i64, _i64, C.POINTER(C.c_int64)],
     "lm_fused_experts": [_v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v,
                          _i64, _v],
+    "lm_fused_experts_noalloc": [_v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v],
     "lm_moe_gate_up": [_v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v],
     "lm_moe_down": [_v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _v, _v],
     "lm_moe_finish": [_v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _v, _i64, _v],

@@ -13,6 +13,7 @@ extern "C" const char *lm_status_string(int status) {
     case LM_EUNSUPPORTED: return "unsupported shape";
     case LM_ELAUNCH: return "kernel launch failed";
     case LM_EWORKSPACE: return "workspace too small";
+    case LM_ETOOLARGE: return "problem exceeds the static no-allocation scratch";
     default: return "unknown status";
   }
 }

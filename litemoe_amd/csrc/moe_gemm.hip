@@ -22,6 +22,8 @@
 //
 // Reference: the expert math of litemoe/ops.py:43-47 (reference_experts) and
 // the vLLM fused_experts call at litemoe/ep.py:40-41.
+#include <mutex>
+
 #include "internal.h"
 
 namespace lm {
@@ -705,6 +707,72 @@ extern "C" int lm_fused_experts(const void *x, const void *w13, const void *w2,
   int rc = run_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows, w.y,
                       w, stream);
   if (rc) return rc;
+  return launch_finish(w.y, topk_ids, nullptr, topk_weights, logical, (bf16 *)out, tokens, hidden,
+                       topk, 0, experts, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// lm_fused_experts_noalloc: the same call with its workspace carved from a
+// static device array instead of a caller buffer, for callers that cannot
+// allocate. Each GPU holds its own copy of the array (at its own address)
+// from the module's load to the end of the process. Nothing in the
+// workspace needs to start at zero: every offset, route list, act and y
+// row a kernel reads is written earlier in the same call, so the previous
+// call's contents never leak into a result. Calls that overlap on one GPU
+// (two streams, or two host threads) share the array and race.
+namespace {
+constexpr int64_t kNoAllocScratchBytes = int64_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void *scratch_ptr[kMaxDevices];  // device address of `scratch` on each device, once looked up
+
+// The array's device address on the current device. In host code the name
+// `scratch` is only a host-side stand-in: it must never reach a kernel or
+// a copy, so every use goes through the looked-up address.
+int scratch_address(int device, void **out) {
+  if (device < 0 || device >= kMaxDevices) return LM_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[device]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LM_ELAUNCH;
+    scratch_ptr[device] = p;
+  }
+  *out = scratch_ptr[device];
+  return LM_OK;
+}
+}  // namespace
+
+extern "C" int lm_fused_experts_noalloc(const void *x, const void *w13, const void *w2,
+                                        const float *topk_weights, const int32_t *topk_ids,
+                                        const int64_t *logical, int64_t tokens, int64_t hidden,
+                                        int64_t inter, int64_t experts, int64_t topk,
+                                        int64_t block_rows, void *out, void *stream) {
+  LM_REQUIRE(tokens >= 0 && topk > 0 && topk <= 8 && topk <= experts && block_rows >= 0 &&
+             block_rows % 16 == 0 && experts <= 511);
+  if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
+  if (carve(nullptr, tokens, topk, hidden, inter, experts, true).bytes > kNoAllocScratchBytes)
+    return LM_ETOOLARGE;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(x && w13 && w2 && topk_weights && topk_ids && out);
+  // The array is looked up with the stream's device current (the caller's
+  // current device must be the stream's).
+  int device = -1, current = -1;
+  if (hipGetDevice(&current) != hipSuccess) return LM_ELAUNCH;
+  if (stream) {
+    if (hipStreamGetDevice((hipStream_t)stream, &device) != hipSuccess) return LM_EINVAL;
+    if (device != current) return LM_EINVAL;
+  } else {
+    device = current;
+  }
+  void *base = nullptr;
+  const int rc = scratch_address(device, &base);
+  if (rc) return rc;
+  ExpertWorkspace w = carve(base, tokens, topk, hidden, inter, experts, true);
+  const int rr = run_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows,
+                            w.y, w, stream);
+  if (rr) return rr;
   return launch_finish(w.y, topk_ids, nullptr, topk_weights, logical, (bf16 *)out, tokens, hidden,
                        topk, 0, experts, (hipStream_t)stream);
 }
