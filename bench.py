@@ -317,14 +317,66 @@ def long_decode_bench(args):
     print(json.dumps(line), flush=True)
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cfg1_inputs():
+    """cfg 1: x [16, 1024] N(0, 1) (seed 1), router [32, 1024], w13 [32, 1024,
+    1024] and w2 [32, 1024, 512] N(0, 0.02) (seed 0), bf16."""
+    from litemoe_amd import synth
+    h, e, i, m = 1024, 32, 512, 16
+    return (synth.normal_bf16((m, h), 1.0, synth.tensor_seed(1, 0)),
+            synth.normal_bf16((e, h), 0.02, synth.tensor_seed(0, 0)),
+            synth.normal_bf16((e, 2 * i, h), 0.02, synth.tensor_seed(0, 1)),
+            synth.normal_bf16((e, h, i), 0.02, synth.tensor_seed(0, 2)))
+
+
+def cfg1_moe_block_ms(threads, inputs, warmups=3, repeats=5):
+    """cfg 1 timed directly: one 1B-shape MoE block (16 tokens, 32 experts
+    top-8, intermediate 512) on LiteMoE's CPU path (router GEMM, topk,
+    softmax, bf16 scales, per-row expert GEMMs, bf16 index_add combine):
+    median of ``repeats`` after ``warmups``, in milliseconds."""
+    import statistics
+
+    import torch
+
+    from oracle import ops
+    torch.set_num_threads(threads)
+    x, wr, w1, w2 = inputs
+    k = 8
+
+    def block():
+        scores = ops.linear_rows(x, wr, True)
+        top, ids = ops.select_topk(scores, k)
+        scales = top.softmax(-1).to(torch.bfloat16).float()
+        return ops.reference_experts(x, ids, scales, w1, w2, singleton=True)
+
+    times = []
+    for n in range(warmups + repeats):
+        t0 = time.perf_counter()
+        block()
+        if n >= warmups:
+            times.append(time.perf_counter() - t0)
+    return statistics.median(times) * 1e3
+
+
 def cpu_baseline(model, cfg, engine, state, layers, batch):
-    """Time the CPU oracle's decode step on ``layers`` of the model's layers
-    (weights and filled KV cache copied from the GPU), extrapolate to all."""
+    """The CPU oracle's decode step (LiteMoE's torch CPU path restated) on
+    ``layers`` of the model's layers, weights and the filled KV cache copied
+    from the GPU, extrapolated to all layers; at 1 thread (the reference's
+    own setting) and at every core this process may use. Plus cfg 1's MoE
+    block timed directly."""
     import torch
 
     from oracle import granite as oracle
-    torch.set_num_threads(min(16, len(os.sched_getaffinity(0))))
-    cores = torch.get_num_threads()
+    all_cores = len(os.sched_getaffinity(0))
 
     def sample(n):
         sub = cfg.__class__(**{**cfg.to_dict(), "num_hidden_layers": n})
@@ -346,14 +398,26 @@ def cpu_baseline(model, cfg, engine, state, layers, batch):
             times.append(time.perf_counter() - t0)
         return min(times)
 
-    t0 = sample(0)
-    tl = sample(layers)
-    step = t0 + (tl - t0) * cfg.num_hidden_layers / layers
-    return dict(value=batch / step, unit="tok/s", cores=cores, kind="port",
+    steps = {}
+    for threads in (1, all_cores):
+        torch.set_num_threads(threads)
+        t0, tl = sample(0), sample(layers)
+        steps[threads] = (t0 + (tl - t0) * cfg.num_hidden_layers / layers, tl)
+    inputs = cfg1_inputs()
+    moe = {threads: cfg1_moe_block_ms(threads, inputs) for threads in (1, all_cores)}
+    torch.set_num_threads(all_cores)
+    step, tl = steps[all_cores]
+    return dict(value=batch / step, unit="tok/s", cores=all_cores, kind="port",
+                value_1_thread=batch / steps[1][0], cpu_model=cpu_model(),
+                cfg1_moe_block_ms={"1_thread": round(moe[1], 2), f"{all_cores}_threads": round(moe[all_cores], 2)},
                 sample=(f"CPU oracle decode step (LiteMoE torch CPU path: per-row bf16 GEMMs, masked attention, "
                         f"index_add combine) at batch {batch}, context {int(state['length'][0])}, timed on "
-                        f"{layers} of {cfg.num_hidden_layers} layers plus embedding/head ({tl:.2f} s per step) "
-                        f"and extrapolated to {cfg.num_hidden_layers} layers ({step:.1f} s per step)"))
+                        f"{layers} of {cfg.num_hidden_layers} layers plus embedding/head ({tl:.2f} s per step on "
+                        f"{all_cores} threads, {steps[1][1]:.2f} s on 1) and extrapolated to "
+                        f"{cfg.num_hidden_layers} layers ({step:.1f} s / {steps[1][0]:.1f} s per step); "
+                        f"value on all {all_cores} cores of sched_getaffinity, value_1_thread at 1 thread "
+                        f"(the reference's setting); cfg 1 MoE block (16 tokens, 1B shape) timed directly, "
+                        f"median of 5 after 3 warm-ups"))
 
 
 def main():
@@ -408,7 +472,7 @@ def main():
         log(f"gate_up {roof['gate_up_us']:.1f} us/launch, fused MoE {roof['fused_us']:.1f} us/layer")
         print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in roof.items()}), flush=True)
         return
-    engine = OptimizedEngine(model, requests, mode="graph", ignore_eos=True)
+    engine = OptimizedEngine(model, requests, mode="graph-async", ignore_eos=True)
     with torch.inference_mode():
         t = time.perf_counter()
         engine.prepare_graph()
@@ -452,7 +516,8 @@ def main():
                 engine.prefill()
             torch.cuda.synchronize()
             cpu = cpu_baseline(model, cfg, engine, snapshot, args.cpu_layers, args.batch)
-            log(f"cpu baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+            log(f"cpu baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads, "
+                f"{cpu['value_1_thread']:.3f} tok/s on 1 ({cpu['cpu_model']}); cfg1 MoE {cpu['cfg1_moe_block_ms']}")
 
     gate_gbs = roof["gate_up_bytes"] / (roof["gate_up_us"] * 1e-6) / 1e9
     fused_gbs = roof["fused_bytes"] / (roof["fused_us"] * 1e-6) / 1e9
@@ -470,7 +535,9 @@ def main():
                                 f"{cfg.intermediate_size}), batch {args.batch}, prompt {args.prompt}, "
                                 f"{args.new_tokens} new tokens, greedy, one hipGraph per decode step"),
                    "global_batch": args.batch, "seq_len": args.prompt, "new_tokens": args.new_tokens,
-                   "capacity": engine.capacity, "parallelism": "single GPU"},
+                   "capacity": engine.capacity, "parallelism": "single GPU",
+                   "timed_contexts": [args.prompt, args.prompt + args.steps - 1],
+                   "mean_context": round(args.prompt + (args.steps - 1) / 2, 1)},
         "roofline": {"bound": "hbm", "kernel": "gate_up_scan_kernel (lm_moe_gate_up)",
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
