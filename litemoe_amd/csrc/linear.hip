@@ -37,7 +37,7 @@ template <int KW, int MB>
 __global__ void __launch_bounds__(kThreads)
 splitk_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w, int M, int N,
               int K, float *__restrict__ part) {
-  __shared__ float red[kWaves][MB][2][4][kWave];
+  __shared__ f32x4 red[kWaves][MB][2][kWave];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
   const int n0 = blockIdx.x * kTileN, s = blockIdx.y;
@@ -65,24 +65,30 @@ splitk_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ 
       c[m][0] = mfma16x16x32(av[m][t], b[0][t], c[m][0]);
       c[m][1] = mfma16x16x32(av[m][t], b[1][t], c[m][1]);
     }
+  // The four waves' accumulators are summed through LDS in wave order, one
+  // 16-byte LDS word per lane and MFMA tile (lane l of a 16x16 tile holds C
+  // rows 4*(l/16) .. +3 of column l%16): thread -> (tile, lane) reads the
+  // four waves' words and stores the four rows of its column.
 #pragma unroll
   for (int m = 0; m < MB; ++m)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red[wave][m][j][i][lane] = c[m][j][i];
+    for (int j = 0; j < 2; ++j) red[wave][m][j][lane] = c[m][j];
   __syncthreads();
-  // Thread -> (row, column) of the MB*16 x 32 tile; C row r of a 16x16 block
-  // is held by lanes 16*(r/4) .. +15 at index r%4.
-  for (int o = threadIdx.x; o < MB * 16 * kTileN; o += kThreads) {
-    const int row = o / kTileN, cc = o % kTileN;
-    if (row >= M) break;
-    const int m = row / 16, r = row % 16, j = cc / 16;
-    const int l = cc % 16 + 16 * (r / 4), i = r % 4;
-    float v = 0.f;
+  constexpr int kGroups = MB * 2 * kWave;
 #pragma unroll
-    for (int q = 0; q < kWaves; ++q) v += red[q][m][j][i][l];
-    part[((int64_t)s * M + row) * N + n0 + cc] = v;
+  for (int g0 = 0; g0 < kGroups; g0 += kThreads) {
+    const int g = g0 + threadIdx.x;
+    if (kGroups % kThreads == 0 || g < kGroups) {
+      const int l = g % kWave, j = (g / kWave) % 2, m = g / (2 * kWave);
+      f32x4 v = red[0][m][j][l];
+#pragma unroll
+      for (int q = 1; q < kWaves; ++q) v += red[q][m][j][l];
+      const int row0 = m * 16 + 4 * (l / 16), col = n0 + 16 * j + l % 16;
+      float *dst = part + ((int64_t)s * M + row0) * N + col;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (row0 + i < M) dst[(int64_t)i * N] = v[i];
+    }
   }
 }
 

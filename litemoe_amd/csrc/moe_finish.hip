@@ -23,12 +23,14 @@ finish_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ ids,
   // Rank of each branch under the key logical*K + j (keys are distinct:
   // j differs). A route that is not owned adds nothing wherever it ranks, so
   // its key uses the raw id and the map is read for owned ids only (an id
-  // outside every rank's range never indexes it).
+  // outside every rank's range never indexes it). The workgroup's threads
+  // share the token, so ids, keys and ranks are uniform (scalar registers)
+  // and the ordered sum below branches uniformly.
   int64_t key[kMaxK];
 #pragma unroll
   for (int j = 0; j < kMaxK; ++j) {
     if (j < topk) {
-      const int64_t e = ids[t * topk + j];
+      const int64_t e = __builtin_amdgcn_readfirstlane(ids[t * topk + j]);
       const bool owned = e - rank * count >= 0 && e - rank * count < count;
       key[j] = (logical && owned ? logical[e] : e) * topk + j;
     } else {
@@ -109,14 +111,15 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
   __shared__ float red[4];
   const int64_t t = blockIdx.x;
   const int nvec = hidden / 8;
-  int idv[kMaxK];
-  float sc[kMaxK];
-#pragma unroll
-  for (int j = 0; j < kMaxK; ++j) {
-    const int64_t r = t * topk + (j < topk ? j : topk - 1);
-    idv[j] = ids[r];
-    sc[j] = scales[r];
-  }
+  const int lane = threadIdx.x % kWave;
+  // The token's route ids and scales, lane j holding route j (lanes past
+  // topk repeat the last): lane-dependent addresses make these vector loads,
+  // issued with the rows below and in flight together. (Uniform addresses
+  // would become scalar loads, which wait one after another through the
+  // scalar cache, each a round trip to memory the previous kernel wrote.)
+  const int64_t rl = t * topk + min(lane, topk - 1);
+  const int id_lane = ids[rl];
+  const float sc_lane = scales[rl];
   u32x4 yv[NN][kMaxK], xv[NN], wv[NN];
 #pragma unroll
   for (int v = 0; v < NN; ++v) {
@@ -129,17 +132,30 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
     xv[v] = reinterpret_cast<const u32x4 *>(x + t * hidden)[i];
     wv[v] = reinterpret_cast<const u32x4 *>(w)[i];
   }
-  int64_t key[kMaxK];
-#pragma unroll
-  for (int j = 0; j < kMaxK; ++j)
-    key[j] = j < topk ? (logical ? logical[idv[j]] : (int64_t)idv[j]) * topk + j : INT64_MAX;
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
+  // Every thread of the workgroup combines the same token, so its route
+  // keys (logical id, branch) are uniform: read from their lanes into scalar
+  // registers, ranked with scalar work, and the ordered sum branches
+  // uniformly on the ranks. Ids lie in [0, experts) (the caller's
+  // contract), so the keys fit 32 bits.
   int order[kMaxK];
+  float sc[kMaxK];
+  {
+    int key[kMaxK];
 #pragma unroll
-  for (int j = 0; j < kMaxK; ++j) {
-    int r = 0;
+    for (int j = 0; j < kMaxK; ++j) {
+      const int id = __builtin_amdgcn_readlane(id_lane, j);
+      sc[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc_lane), j));
+      const int lid = logical ? (int)logical[id] : id;
+      key[j] = j < topk ? lid * kMaxK + j : INT_MAX;
+    }
 #pragma unroll
-    for (int i = 0; i < kMaxK; ++i) r += key[i] < key[j];
-    order[j] = r;
+    for (int j = 0; j < kMaxK; ++j) {
+      int r = 0;
+#pragma unroll
+      for (int i = 0; i < kMaxK; ++i) r += key[i] < key[j];
+      order[j] = r;
+    }
   }
   float xn[NN][8];
   float ss = 0.f;
@@ -147,25 +163,28 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
   for (int v = 0; v < NN; ++v) {
     const int i = threadIdx.x + v * 256;
     if (i >= nvec) continue;
-    float contrib[kMaxK][8];
-#pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-      const float s = round_bf16(sc[j]);
-      float f[8];
-      unpack8(yv[v][j], f);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) contrib[j][c] = j < topk ? round_bf16(f[c] * s) : 0.f;
-    }
     float total[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int q = 0; q < kMaxK; ++q) {
+    for (int q = 0; q < topk; ++q) {
 #pragma unroll
       for (int j = 0; j < kMaxK; ++j) {
-        if (order[j] == q) {
+        if (order[j] == q) {  // uniform
+          const float s = round_bf16(sc[j]);
+          float f[8];
+          unpack8(yv[v][j], f);
+          u32x4 p;
 #pragma unroll
-          for (int c = 0; c < 8; ++c) total[c] += contrib[j][c];
+          for (int c = 0; c < 4; ++c) p[c] = pack_bf16(f[2 * c] * s, f[2 * c + 1] * s);
+          float term[8];
+          unpack8(p, term);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) total[c] += term[c];
         }
       }
+    }
+    if (topk < kMaxK) {
+      // the unused branch slots rank last and add +0 (finish_kernel's sum)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) total[c] += 0.f;
     }
     float xf[8];
     unpack8(xv[v], xf);
