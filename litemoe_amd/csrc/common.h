@@ -90,6 +90,24 @@ __device__ __forceinline__ float dpp_sum8(float v) {
   return v;
 }
 
+// acc + the dot product of the eight bf16 values of two 16-byte words: four
+// v_dot2_f32_bf16 in channel-pair order (each adds two exact bf16 products).
+// The pairs are taken with shufflevector from a bf16x8 view: bit-casting the
+// indexed u32 elements inside an unrolled loop compiles to four dots of
+// element 0.
+__device__ __forceinline__ float dot8_bf16_acc(const u32x4 &a, const u32x4 &b, float acc) {
+  const bf16x8 av = as_bf16x8(a), bv = as_bf16x8(b);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 0, 1),
+                                        __builtin_shufflevector(bv, bv, 0, 1), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 2, 3),
+                                        __builtin_shufflevector(bv, bv, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 4, 5),
+                                        __builtin_shufflevector(bv, bv, 4, 5), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 6, 7),
+                                        __builtin_shufflevector(bv, bv, 6, 7), acc, false);
+  return acc;
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
 // MFMA 16x16x32 bf16 (gfx950). Lane l supplies row l%16 of A and column l%16

@@ -40,8 +40,7 @@ __device__ void router_gemv(const u32x4 *zs, const bf16 *__restrict__ wr, int nv
 #pragma unroll
     for (int b = 0; b < kExpertBatch; ++b) acc[b] = 0.f;
     for (int i = lane; i < nvec; i += kWave) {
-      float zf[8];
-      unpack8(zs[i], zf);
+      const u32x4 zw = zs[i];
       u32x4 w[kExpertBatch];
 #pragma unroll
       for (int b = 0; b < kExpertBatch; ++b) {
@@ -50,12 +49,7 @@ __device__ void router_gemv(const u32x4 *zs, const bf16 *__restrict__ wr, int nv
         w[b] = reinterpret_cast<const u32x4 *>(wr + (int64_t)ee * nvec * 8)[i];
       }
 #pragma unroll
-      for (int b = 0; b < kExpertBatch; ++b) {
-        float wf[8];
-        unpack8(w[b], wf);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc[b] = fmaf(zf[c], wf[c], acc[b]);
-      }
+      for (int b = 0; b < kExpertBatch; ++b) acc[b] = dot8_bf16_acc(zw, w[b], acc[b]);
     }
 #pragma unroll
     for (int b = 0; b < kExpertBatch; ++b) {
@@ -102,15 +96,16 @@ __device__ void select_topk(const float *logit, int experts, int topk, int renor
 }
 
 // select_topk for experts <= 64, run by wave 0 alone with no barrier: logits
-// are bf16, so (orderable bf16 bits, ~id) fits a 32-bit key. Lane e computes
-// expert e's key, publishes it to LDS and counts the larger keys among all
-// 64 read back as broadcasts (every lane reads the same address: no readlane
-// chain); the lane of rank 0 is found with a ballot, and the softmax terms of
-// the selection are summed in rank order through LDS. logit[kWave, 3*kWave)
-// is scratch. The selection, the weights and the order of the softmax
-// denominator's sum are those of select_topk. The caller synchronises before
-// (logits in LDS). select_topk_lanes is the same selection for any one wave
-// of the workgroup, with its own 2*kWave floats of LDS scratch.
+// are bf16, so (orderable bf16 bits, ~id) fits a 32-bit key, distinct per
+// expert. Lane e holds expert e's key; rank r goes to the lane holding the
+// wave's largest remaining key (a DPP maximum within rows of 16, then the
+// four row maxima as scalars), which then drops out: topk rounds of register
+// work, no LDS traffic. The softmax terms of the selection are summed in
+// rank order through LDS. logit[kWave, 3*kWave) is scratch. The selection,
+// the weights and the order of the softmax denominator's sum are those of
+// select_topk. The caller synchronises before (logits in LDS).
+// select_topk_lanes is the same selection for any one wave of the
+// workgroup, with its own 2*kWave floats of LDS scratch.
 __device__ __forceinline__ uint32_t select_key32(float v, int id) {
   uint32_t h = __float_as_uint(v) >> 16;  // exact: logits are bf16 values
   if ((h & 0x7fffu) > 0x7f80u) h = 0x7fc0u;
@@ -118,23 +113,29 @@ __device__ __forceinline__ uint32_t select_key32(float v, int id) {
   return (ord << 16) | (0xffffu - (uint32_t)id);
 }
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true));
+  return max(max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
+             max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
+}
+
 __device__ void select_topk_lanes(const float *logit, float *scratch, int t, int experts,
                                   int topk, int renormalize, float *__restrict__ tw,
                                   int32_t *__restrict__ tid) {
   const float v = logit[min(t, experts - 1)];
-  const uint32_t key = t < experts ? select_key32(v, t) : 0u;  // 0: below every real key
-  // Each lane publishes its key once; every lane then compares against all
-  // 64 (broadcast reads, padding keys are 0 and never larger).
-  uint32_t *keys = reinterpret_cast<uint32_t *>(scratch);
+  uint32_t key = t < experts ? select_key32(v, t) : 0u;  // 0: below every real key
   float *terms = scratch + kWave;
-  keys[t] = key;
-  int rank = 0;
-#pragma unroll
-  for (int e4 = 0; e4 < kWave / 4; ++e4) {
-    const uint4 k4 = *reinterpret_cast<const uint4 *>(keys + 4 * e4);
-    rank += (k4.x > key) + (k4.y > key) + (k4.z > key) + (k4.w > key);
+  int rank = kWave;  // not selected
+  for (int r = 0; r < topk; ++r) {
+    const uint32_t top_key = wave_max_u32(key);
+    if (key == top_key) {  // exactly one lane: keys are distinct
+      rank = r;
+      key = 0u;
+    }
   }
-  if (t >= experts) rank = kWave;
   const int top = __builtin_ctzll(__ballot(rank == 0));
   const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
   const float ex = expf(v - m);
@@ -317,17 +318,12 @@ __device__ __forceinline__ void gate_round(const u32x4 *zs, int experts, int rou
 #pragma unroll
   for (int b = 0; b < FastRouter<NV>::kBatch; ++b) {
     const int e = round * FastRouter<NV>::kRound + wave + b * kFastWaves;
+    if (e >= experts) continue;  // uniform across the wave
     float acc = 0.f;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      float zf[8], wf[8];
-      unpack8(zs[lane + v * kWave], zf);
-      unpack8(w[b][v], wf);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) acc = fmaf(zf[c], wf[c], acc);
-    }
+    for (int v = 0; v < NV; ++v) acc = dot8_bf16_acc(zs[lane + v * kWave], w[b][v], acc);
     const float sum = wave_sum(acc);
-    if (lane == 0 && e < experts) {
+    if (lane == 0) {
       const uint32_t h = f32_to_bf16(sum);
       logit[e] = bf16_to_f32(h);
       if (logits_row) logits_row[e] = (bf16)h;
