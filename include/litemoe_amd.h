@@ -455,14 +455,19 @@ int lm_decode_prologue(const uint8_t *active, const int64_t *length,
  * stored, with system-scope stores, into slot (*step_counter - 1) %
  * ring_depth, step_counter being the device counter lm_decode_prologue
  * increments. This folds the per-step device-to-host copy of the
- * reference's OutputRing (litemoe/execution.py:25-41) into the step. */
+ * reference's OutputRing (litemoe/execution.py:25-41) into the step.
+ * workspace: lm_greedy_epilogue_workspace_size bytes (the argmax of each
+ * row is split over slices of the row; two launches). rows <= 65535. */
+int lm_greedy_epilogue_workspace_size(int64_t rows, int64_t vocab,
+                                      int64_t *bytes);
 int lm_greedy_epilogue(const void *logits, int64_t ld, float logits_scaling,
                        int64_t vocab, int64_t rows, const uint8_t *valid,
                        int64_t *next, int64_t *length, int64_t *generated,
                        const int64_t *budget, uint8_t *active, int64_t *emit,
                        const int64_t *eos, int64_t neos, int ignore_eos,
                        int64_t *emit_ring, int64_t ring_depth,
-                       const int64_t *step_counter, void *stream);
+                       const int64_t *step_counter, void *workspace,
+                       int64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -55,8 +55,9 @@ _SIGNATURES = {
                                      _i32, _v, _v, _v, _v],
     "lm_decode_prologue": [_v, _v, _v, _v, _f32, _v, _f32, _v, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64,
                            _v],
+    "lm_greedy_epilogue_workspace_size": [_i64, _i64, C.POINTER(C.c_int64)],
     "lm_greedy_epilogue": [_v, _i64, _f32, _i64, _i64, _v, _v, _v, _v, _v, _v, _v, _v, _i64, _i32,
-                           _v, _i64, _v, _v],
+                           _v, _i64, _v, _v, _i64, _v],
     "lm_host_device_pointer": [_v, C.POINTER(C.c_void_p)],
 }
 _RESTYPE = {"lm_version": C.c_char_p, "lm_status_string": C.c_char_p}

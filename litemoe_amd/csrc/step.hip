@@ -119,112 +119,114 @@ prologue_kernel(const uint8_t *__restrict__ active, const int64_t *__restrict__ 
   }
 }
 
-constexpr int kArgThreads = 1024;
-constexpr int kArgChunks = 8;  // 16-byte loads per lane in flight
+// The argmax of a logits row is split over `parts` workgroups per row, each
+// scanning a slice of the row's aligned 16-byte chunks, so the whole GPU
+// takes part (one workgroup per row leaves most CUs idle and the scan's VALU
+// work serial). A slice's result is one 64-bit word: (key + 1) << 32 |
+// (0xffffffff - index), key the orderable bf16 of the scaled value (NaN
+// above everything, -0 equal to +0). The largest word is the largest value
+// at its lowest index (torch.argmax); 0 means an empty slice. The state
+// update then reduces the row's words.
+constexpr int kArgThreads = 256;
+constexpr int kArgChunks = 2;  // 16-byte loads per lane per round (a slice is about two per lane)
 
-// (value, index) order of torch.argmax: larger value first, then lower index;
-// NaN above everything (torch.argmax returns the first NaN).
-__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
-  const bool na = a != a, nb = b != b;
-  if (na != nb) return na;
-  if (!na && a != b) return a > b;
-  return ia < ib;
+__device__ __forceinline__ uint64_t pack_best(uint32_t key1, int index) {
+  return ((uint64_t)key1 << 32) | (uint64_t)(0xffffffffu - (uint32_t)index);
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, off, kWave);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, kWave);
+    v = max_u64(v, ((uint64_t)hi << 32) | lo);
+  }
+  return v;
 }
 
 __global__ void __launch_bounds__(kArgThreads)
-epilogue_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, int vocab,
-                const uint8_t *__restrict__ valid, int64_t *__restrict__ next,
-                int64_t *__restrict__ length, int64_t *__restrict__ generated,
-                const int64_t *__restrict__ budget, uint8_t *__restrict__ active,
-                int64_t *__restrict__ emit, const int64_t *__restrict__ eos, int neos,
-                int ignore_eos, int64_t *__restrict__ ring, int64_t depth,
-                const int64_t *__restrict__ step_counter) {
-  __shared__ float sv[kArgThreads / kWave];
-  __shared__ int si[kArgThreads / kWave];
-  const int64_t row = blockIdx.x;
+argmax_part_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, int vocab,
+                   int parts, uint64_t *__restrict__ best_out) {
+  __shared__ uint64_t sb[kArgThreads / kWave];
+  const int64_t row = blockIdx.y;
+  const int part = blockIdx.x;
   // The row is read in aligned 16-byte chunks (rows of an odd vocab start
   // anywhere): chunk c holds values 8c - lead .. 8c - lead + 7, and only
   // those in [0, vocab) count. An aligned chunk never leaves the page of the
   // row value it holds.
   const bf16 *lr = logits + row * ld;
-  const int mis = (int)(reinterpret_cast<uintptr_t>(lr) & 15);  // bytes past the last 16-byte boundary
+  const int mis = (int)(reinterpret_cast<uintptr_t>(lr) & 15);
   const u32x4 *chunks = reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(lr) - mis);
   const int lead = mis / 2;
   const int nchunks = (lead + vocab + 7) / 8;
+  const int per = (nchunks + parts - 1) / parts;
+  const int c0 = part * per, c1 = min(nchunks, c0 + per);
   // A lane visits its values in increasing index order, so a strict
-  // comparison of orderable keys (NaN above everything) keeps the first
-  // index of its maximum; lanes and waves then merge with better().
-  uint32_t bk = 0;  // below every real key
-  int bi = vocab;   // none yet
+  // comparison of orderable keys keeps the first index of its maximum.
+  uint32_t bk = 0;  // key + 1 of the best so far (0: none)
+  int bi = vocab;
   u32x4 raw[kArgChunks];
-  auto load = [&](int base) {
+  for (int base = c0 + threadIdx.x; base < c1; base += kArgThreads * kArgChunks) {
+    // every chunk load of the round before any arithmetic (clamped indices,
+    // masked below)
 #pragma unroll
-    for (int u = 0; u < kArgChunks; ++u) raw[u] = chunks[min(base + u * kArgThreads, nchunks - 1)];
-  };
-  auto scan = [&](int base) {
+    for (int u = 0; u < kArgChunks; ++u) raw[u] = chunks[min(base + u * kArgThreads, c1 - 1)];
 #pragma unroll
     for (int u = 0; u < kArgChunks; ++u) {
       float f[8];
       unpack8(raw[u], f);
-      const int v0 = (base + u * kArgThreads) * 8 - lead;
+      const int c = base + u * kArgThreads;
+      const int v0 = c * 8 - lead;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int v = v0 + j;
-        uint32_t h = f32_to_bf16(f[j] * inv_scaling);
-        h = h == 0x8000u ? 0u : h;  // -0 ties with +0, as in a float compare
-        const uint32_t key = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);  // NaN is 0x7fc0: top
-        const bool in = base + u * kArgThreads < nchunks && v >= 0 && v < vocab;
-        if (in && key + 1u > bk) {  // key + 1 > 0 for every real value
-          bk = key + 1u;
-          bi = v;
+      for (int j = 0; j < 4; ++j) {
+        // two values per conversion (v_cvt_pk_bf16_f32, NaN made 0x7fc0)
+        const uint32_t pair = pack_bf16(f[2 * j] * inv_scaling, f[2 * j + 1] * inv_scaling);
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          uint32_t h = h2 ? pair >> 16 : pair & 0xffffu;
+          const int v = v0 + 2 * j + h2;
+          h = h == 0x8000u ? 0u : h;  // -0 ties with +0, as in a float compare
+          const uint32_t key = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);  // NaN 0x7fc0: top
+          const bool in = c < c1 && v >= 0 && v < vocab;
+          if (in && key + 1u > bk) {
+            bk = key + 1u;
+            bi = v;
+          }
         }
       }
     }
-  };
-  // First round (rows up to 8 * kArgThreads * kArgChunks values): every
-  // chunk load, then the row's state, are issued before anything waits; the
-  // state is used only at the end. eos may be NULL when neos == 0: the row's
-  // own counter is read instead.
-  load(threadIdx.x);
-  const bool val = valid[row] != 0;
-  const int64_t gen = generated[row], len = length[row], bud = budget[row];
-  const int64_t eos_read = *(neos > 0 ? eos : generated + row);
-  __builtin_amdgcn_sched_barrier(0);
-  scan(threadIdx.x);
-  for (int base = threadIdx.x + kArgThreads * kArgChunks; base < nchunks;
-       base += kArgThreads * kArgChunks) {
-    load(base);
-    scan(base);
   }
-  const int64_t eos_first = neos > 0 ? eos_read : -1;
-  float best = -INFINITY;
-  if (bi < vocab) {
-    const uint32_t key = bk - 1u;
-    best = bf16_to_f32((key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu));
-  }
-  // Wave then workgroup reduction of (value, index).
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(best, off, kWave);
-    const int oi = __shfl_xor(bi, off, kWave);
-    if (better(ov, oi, best, bi)) {
-      best = ov;
-      bi = oi;
-    }
-  }
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  if (lane == 0) {
-    sv[wave] = best;
-    si[wave] = bi;
-  }
+  uint64_t b = wave_max_u64(bk ? pack_best(bk, bi) : 0ull);
+  if (threadIdx.x % kWave == 0) sb[threadIdx.x / kWave] = b;
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kArgThreads / kWave; ++w)
-      if (better(sv[w], si[w], best, bi)) {
-        best = sv[w];
-        bi = si[w];
-      }
-    const int64_t candidate = bi;
+#pragma unroll
+    for (int w = 1; w < kArgThreads / kWave; ++w) b = max_u64(b, sb[w]);
+    best_out[row * parts + part] = b;
+  }
+}
+
+// The row's slice results reduced to the candidate token, then the emit row
+// and the engine's state update (one wave per row).
+__global__ void __launch_bounds__(kWave)
+greedy_update_kernel(const uint64_t *__restrict__ best, int parts, const uint8_t *__restrict__ valid,
+                     int64_t *__restrict__ next, int64_t *__restrict__ length,
+                     int64_t *__restrict__ generated, const int64_t *__restrict__ budget,
+                     uint8_t *__restrict__ active, int64_t *__restrict__ emit,
+                     const int64_t *__restrict__ eos, int neos, int ignore_eos,
+                     int64_t *__restrict__ ring, int64_t depth,
+                     const int64_t *__restrict__ step_counter) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  uint64_t b = 0;
+  for (int p = lane; p < parts; p += kWave) b = max_u64(b, best[row * parts + p]);
+  b = wave_max_u64(b);
+  if (lane == 0) {
+    const int64_t candidate = (int64_t)(0xffffffffu - (uint32_t)b);
+    const bool val = valid[row] != 0;
+    const int64_t gen = generated[row];
     emit[row * 3 + 0] = candidate;
     emit[row * 3 + 1] = gen;
     emit[row * 3 + 2] = val;
@@ -236,17 +238,18 @@ epilogue_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scaling, 
       __hip_atomic_store(dst + 2, (int64_t)val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     const int64_t gen1 = gen + (val ? 1 : 0);
-    length[row] = len + (val ? 1 : 0);
+    length[row] += val ? 1 : 0;
     generated[row] = gen1;
     if (val) next[row] = candidate;
-    bool done = gen1 >= bud;
-    if (!ignore_eos && neos > 0) {
-      done = done || candidate == eos_first;
-      for (int e = 1; e < neos; ++e) done = done || candidate == eos[e];
-    }
+    bool done = gen1 >= budget[row];
+    if (!ignore_eos)
+      for (int e = 0; e < neos; ++e) done = done || candidate == eos[e];
     active[row] = val && !done;
   }
 }
+
+// Slices per row: about 4096 values each, at most 64.
+int arg_parts(int64_t vocab) { return (int)max((int64_t)1, min((int64_t)64, cdiv(vocab, 4096))); }
 
 }  // namespace
 }  // namespace lm
@@ -270,22 +273,36 @@ extern "C" int lm_decode_prologue(const uint8_t *active, const int64_t *length, 
   return LM_OK;
 }
 
+extern "C" int lm_greedy_epilogue_workspace_size(int64_t rows, int64_t vocab, int64_t *bytes) {
+  LM_REQUIRE(bytes && rows >= 0 && vocab > 0);
+  *bytes = rows * arg_parts(vocab) * 8;
+  return LM_OK;
+}
+
 extern "C" int lm_greedy_epilogue(const void *logits, int64_t ld, float logits_scaling,
                                   int64_t vocab, int64_t rows, const uint8_t *valid,
                                   int64_t *next, int64_t *length, int64_t *generated,
                                   const int64_t *budget, uint8_t *active, int64_t *emit,
                                   const int64_t *eos, int64_t neos, int ignore_eos,
                                   int64_t *emit_ring, int64_t ring_depth,
-                                  const int64_t *step_counter, void *stream) {
+                                  const int64_t *step_counter, void *workspace,
+                                  int64_t workspace_bytes, void *stream) {
   LM_REQUIRE(rows >= 0 && vocab > 0 && vocab < ((int64_t)1 << 31) && ld >= vocab && neos >= 0 &&
-             logits_scaling > 0.f && (!emit_ring || (ring_depth > 0 && step_counter)));
+             logits_scaling > 0.f && (!emit_ring || (ring_depth > 0 && step_counter)) &&
+             rows <= 65535);
   if (rows == 0) return LM_OK;
   LM_REQUIRE(logits && valid && next && length && generated && budget && active && emit &&
-             (neos == 0 || eos));
-  const float inv_scaling = 1.0f / logits_scaling;
-  epilogue_kernel<<<dim3((unsigned)rows), kArgThreads, 0, (hipStream_t)stream>>>(
-      (const bf16 *)logits, ld, inv_scaling, (int)vocab, valid, next, length, generated,
-      budget, active, emit, eos, (int)neos, ignore_eos, emit_ring, ring_depth, step_counter);
+             (neos == 0 || eos) && workspace);
+  const int parts = arg_parts(vocab);
+  if (workspace_bytes < rows * parts * 8) return LM_EWORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  uint64_t *best = static_cast<uint64_t *>(workspace);
+  argmax_part_kernel<<<dim3((unsigned)parts, (unsigned)rows), kArgThreads, 0, s>>>(
+      (const bf16 *)logits, ld, 1.0f / logits_scaling, (int)vocab, parts, best);
+  LM_CHECK_LAUNCH();
+  greedy_update_kernel<<<dim3((unsigned)rows), kWave, 0, s>>>(
+      best, parts, valid, next, length, generated, budget, active, emit, eos, (int)neos,
+      ignore_eos, emit_ring, ring_depth, step_counter);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

@@ -83,9 +83,11 @@ def greedy_epilogue(logits, logits_scaling, valid, state, emit, eos, ignore_eos,
     if eos.dtype != torch.int64 or not eos.is_contiguous():
         raise ValueError("eos must be a contiguous int64 tensor")
     ring_ptr, depth, counter = (None, 0, None) if ring_target is None else ring_target
+    nbytes = _lib.size_query("lm_greedy_epilogue_workspace_size", rows, vocab)
+    ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=logits.device)
     _lib.call("lm_greedy_epilogue", logits.data_ptr(), logits.stride(0), float(logits_scaling), vocab,
               rows, _bool_bytes(valid).data_ptr(), state["next"].data_ptr(), state["length"].data_ptr(),
               state["generated"].data_ptr(), state["budget"].data_ptr(),
               _bool_bytes(state["active"]).data_ptr(), emit.data_ptr(),
               eos.data_ptr() if eos.numel() else None, eos.numel(), int(bool(ignore_eos)),
-              ring_ptr, depth, _lib.ptr(counter), _lib.stream(logits.device))
+              ring_ptr, depth, _lib.ptr(counter), ws.data_ptr(), ws.numel(), _lib.stream(logits.device))
