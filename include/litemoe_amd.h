@@ -469,6 +469,44 @@ int lm_greedy_epilogue(const void *logits, int64_t ld, float logits_scaling,
                        const int64_t *step_counter, void *workspace,
                        int64_t workspace_bytes, void *stream);
 
+/* The LM head in MFMA fragment order, for lm_head_greedy (one launch;
+ * done once when the model is loaded): 16-byte chunk (k, tile, lane) of
+ * packed = head[16*tile + lane%16][32*k + 8*(lane/16) .. +8], k-steps of
+ * 32 outermost, then tiles of 16 vocabulary rows; zero rows past the
+ * vocabulary.
+ * lm_head_pack_size: ceil(vocab/16)*16*hidden*2 bytes. head bf16
+ * [vocab][hidden] contiguous; hidden a multiple of 32. No counterpart in the
+ * reference, which multiplies by the checkpoint layout (model.py:127). */
+int lm_head_pack_size(int64_t vocab, int64_t hidden, int64_t *bytes);
+int lm_head_pack(const void *head, int64_t vocab, int64_t hidden, void *packed,
+                 void *stream);
+
+/* The LM head product and lm_greedy_epilogue fused (two launches):
+ *   logits[b][v] = bf16(sum_k z[b][k] * head[v][k])   (F.linear's output)
+ * then the candidate, emit row and state update exactly as
+ * lm_greedy_epilogue computes them from those logits. The head weights are
+ * streamed once, with the argmax of each vocabulary slice taken in the
+ * product's epilogue; the logits are stored only if `logits` is not NULL
+ * (bf16 [rows][ldo]). Replaces litemoe/model.py:127 (F.linear(z, head) /
+ * logits_scaling) and engine.py:92-102. z: bf16 [rows][ldz], 16-byte
+ * aligned, ldz a multiple of 8; head: the lm_head_pack layout of the bf16
+ * [vocab][hidden] head, 16-byte aligned. rows <= 128 and hidden in {512, 1024, 1536, 2048}
+ * (else LM_EUNSUPPORTED). The fp32 sum runs in the MFMA's order, so a
+ * logit may differ from another BLAS's by one bf16 ulp; the candidate is
+ * always the argmax of the logits this call computes. Ring arguments as
+ * lm_greedy_epilogue; workspace: lm_head_greedy_workspace_size bytes. */
+int lm_head_greedy_workspace_size(int64_t rows, int64_t vocab, int64_t hidden,
+                                  int64_t *bytes);
+int lm_head_greedy(const void *z, int64_t ldz, const void *head, int64_t rows,
+                   int64_t vocab, int64_t hidden, float logits_scaling,
+                   void *logits, int64_t ldo, const uint8_t *valid,
+                   int64_t *next, int64_t *length, int64_t *generated,
+                   const int64_t *budget, uint8_t *active, int64_t *emit,
+                   const int64_t *eos, int64_t neos, int ignore_eos,
+                   int64_t *emit_ring, int64_t ring_depth,
+                   const int64_t *step_counter, void *workspace,
+                   int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

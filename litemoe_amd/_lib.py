@@ -59,6 +59,11 @@ _SIGNATURES = {
     "lm_greedy_epilogue": [_v, _i64, _f32, _i64, _i64, _v, _v, _v, _v, _v, _v, _v, _v, _i64, _i32,
                            _v, _i64, _v, _v, _i64, _v],
     "lm_host_device_pointer": [_v, C.POINTER(C.c_void_p)],
+    "lm_head_pack_size": [_i64, _i64, C.POINTER(C.c_int64)],
+    "lm_head_pack": [_v, _i64, _i64, _v, _v],
+    "lm_head_greedy_workspace_size": [_i64, _i64, _i64, C.POINTER(C.c_int64)],
+    "lm_head_greedy": [_v, _i64, _v, _i64, _i64, _i64, _f32, _v, _i64, _v, _v, _v, _v, _v, _v, _v, _v,
+                       _i64, _i32, _v, _i64, _v, _v, _i64, _v],
 }
 _RESTYPE = {"lm_version": C.c_char_p, "lm_status_string": C.c_char_p}
 

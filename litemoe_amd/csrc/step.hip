@@ -136,6 +136,13 @@ __device__ __forceinline__ uint64_t pack_best(uint32_t key1, int index) {
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+// Orderable key of a bf16 value: larger value, larger key; -0 equal to +0;
+// the canonical NaN 0x7fc0 above every number.
+__device__ __forceinline__ uint32_t order_key(uint32_t h) {
+  h = h == 0x8000u ? 0u : h;
+  return (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) {
@@ -185,10 +192,9 @@ argmax_part_kernel(const bf16 *__restrict__ logits, int64_t ld, float inv_scalin
         const uint32_t pair = pack_bf16(f[2 * j] * inv_scaling, f[2 * j + 1] * inv_scaling);
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
-          uint32_t h = h2 ? pair >> 16 : pair & 0xffffu;
+          const uint32_t h = h2 ? pair >> 16 : pair & 0xffffu;
           const int v = v0 + 2 * j + h2;
-          h = h == 0x8000u ? 0u : h;  // -0 ties with +0, as in a float compare
-          const uint32_t key = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);  // NaN 0x7fc0: top
+          const uint32_t key = order_key(h);
           const bool in = c < c1 && v >= 0 && v < vocab;
           if (in && key + 1u > bk) {
             bk = key + 1u;
@@ -251,6 +257,235 @@ greedy_update_kernel(const uint64_t *__restrict__ best, int parts, const uint8_t
 // Slices per row: about 4096 values each, at most 64.
 int arg_parts(int64_t vocab) { return (int)max((int64_t)1, min((int64_t)64, cdiv(vocab, 4096))); }
 
+// The LM head product with the greedy argmax in its epilogue: one launch
+// streams the head weights [vocab, hidden] once and leaves, per row and
+// workgroup, the best (key, index) word of the workgroup's vocabulary
+// slice, in argmax_part_kernel's format; greedy_update_kernel then reduces
+// the words and updates the state. The raw head output (F.linear's bf16
+// logits) is never written unless the caller asks for it.
+//
+// Workgroup = 4 waves over a slice of 4*TW vocabulary tiles of 16 rows;
+// every wave owns TW tiles and all M (<= 16*MB) rows, so no partial sums
+// cross waves. The head rows are the MFMA B operand, read from the head in
+// fragment order, k-step major (lm_head_pack: each wave load is 1 KB
+// contiguous, a wave's TW tiles of one k-step are adjacent, and all the
+// workgroups of a k-step read one contiguous block of vocab*64 bytes, so
+// the DRAM sees a front sweeping through memory rather than 64 bytes of 48
+// rows at a time) into a register ring kHeadDepth k-steps ahead. The rows
+// z [M, hidden] are the A
+// operand, read from LDS, where they are staged in phases of KP k-steps
+// (at most 32 KB, two buffers; 16-byte chunk c of row r at c ^ (r & 15),
+// conflict-free).
+// Vector loads complete in issue order, so the loads of phase p+1 are
+// issued right behind the head loads of k-step (p+1)*KP: waiting for them at
+// the end of phase p then waits for no head load that is not due next, and
+// the head stream never drains. Per lane: C rows 4*(l/16)+i of vocabulary
+// column l%16 of a tile. logits = bf16(sum) (one rounding, as F.linear's
+// output); the argmax key is that of bf16(logits * (1 / logits_scaling)),
+// as in argmax_part_kernel, so the candidate equals lm_greedy_epilogue's
+// over the same logits.
+constexpr int kHeadWaves = 4;
+constexpr int kHeadThreads = kHeadWaves * kWave;
+// Tuning knobs (compile-time): k-steps of head loads in flight per wave,
+// LDS bytes for one phase of z.
+#ifndef LM_HEAD_DEPTH
+#define LM_HEAD_DEPTH 4
+#endif
+#ifndef LM_HEAD_PHASE_KB
+#define LM_HEAD_PHASE_KB 16
+#endif
+constexpr int kHeadDepth = LM_HEAD_DEPTH;
+constexpr int kHeadPhaseBytes = LM_HEAD_PHASE_KB << 10;
+
+__device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+template <int MB>
+constexpr int head_tiles_per_wave() { return MB <= 4 ? 3 : 2; }
+
+// k-steps per phase: the largest divisor of KS whose phase fits the LDS
+// budget (a k-step of z is MB*16 rows x 64 bytes).
+// (at least 4, the k-steps of one swizzle row of 16 chunks)
+template <int MB, int KS>
+constexpr int head_phase_steps() {
+  int kp = KS;
+  while (kp > 4 && (KS % kp != 0 || MB * 16 * kp * 64 > kHeadPhaseBytes || kp % 4 != 0)) --kp;
+  return kp;
+}
+
+template <int MB, int KS>
+__global__ void __launch_bounds__(kHeadThreads)
+head_argmax_kernel(const bf16 *__restrict__ z, int64_t ldz, const bf16 *__restrict__ head,
+                   int M, int vocab, float inv_scaling, bf16 *__restrict__ logits, int64_t ldo,
+                   uint64_t *__restrict__ best_out) {
+  constexpr int TW = head_tiles_per_wave<MB>();
+  constexpr int kRows = MB * 16;
+  constexpr int KP = head_phase_steps<MB, KS>();
+  constexpr int NP = KS / KP;
+  constexpr int kChunksPerRow = KP * 4;                         // 16-byte chunks of a phase row
+  constexpr int kPer = kRows * kChunksPerRow / kHeadThreads;    // chunks per thread and phase
+  constexpr int D = kHeadDepth < KS ? kHeadDepth : KS;
+  // phase p+1 is issued behind the head loads of k-step (p+1)*KP, i.e. after
+  // computing k-step (p+1)*KP - D (at the start of phase p if KP <= D)
+  constexpr int kIssueAt = KP > D ? KP - D : 0;
+  static_assert(KS % KP == 0 && KP % 4 == 0 && kPer >= 1 &&
+                kRows * kChunksPerRow % kHeadThreads == 0, "phase shape");
+  __shared__ u32x4 abuf[2][kRows * kChunksPerRow];
+  __shared__ uint64_t wbest[kHeadWaves][kRows];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int col = lane % 16, grp = lane / 16;
+  const int tile0 = ((int)blockIdx.x * kHeadWaves + wave) * TW;
+  const int tiles = (vocab + 15) / 16;
+  const bf16 *wp[TW];
+#pragma unroll
+  for (int t = 0; t < TW; ++t) {
+    // tiles past the vocabulary repeat the last one (loads stay in bounds;
+    // those columns are masked below)
+    const int tile = min(tile0 + t, tiles - 1);
+    wp[t] = head + ((int64_t)tile * kWave + lane) * 8;
+  }
+  // D + 1 slots: the refill of k-step ks + D is issued before the MFMAs of
+  // k-step ks, into a slot those MFMAs do not read.
+  u32x4 ring[D + 1][TW];
+  u32x4 ra[kPer];
+  auto load_b = [&](int ks) {
+#pragma unroll
+    for (int t = 0; t < TW; ++t) ring[ks % (D + 1)][t] = load16(wp[t] + (int64_t)ks * tiles * kWave * 8);
+  };
+  auto load_a = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int q = (int)threadIdx.x + i * kHeadThreads;
+      const int row = q / kChunksPerRow, c = q % kChunksPerRow;
+      ra[i] = load16(z + (int64_t)min(row, M - 1) * ldz + p * KP * 32 + c * 8);
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int q = (int)threadIdx.x + i * kHeadThreads;
+      const int row = q / kChunksPerRow, c = q % kChunksPerRow;
+      abuf[buf][row * kChunksPerRow + (c ^ (row & 15))] = ra[i];
+    }
+  };
+  load_a(0);
+#pragma unroll
+  for (int ks = 0; ks < D; ++ks) load_b(ks);
+  store_a(0);
+  __syncthreads();
+  f32x4 acc[TW][MB];
+#pragma unroll
+  for (int t = 0; t < TW; ++t)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[t][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int p = ks / KP, j = ks % KP;
+    if (NP > 1 && p + 1 < NP && j == kIssueAt && kIssueAt == 0) load_a(p + 1);
+    if (ks + D < KS) load_b(ks + D);
+    if (NP > 1 && p + 1 < NP && j == kIssueAt && kIssueAt > 0) load_a(p + 1);
+    // Keep the refill ahead of the MFMAs: left alone, the scheduler sinks
+    // the loads below later k-steps' MFMAs and the ring drains.
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 a[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+      a[m] = abuf[p & 1][(m * 16 + col) * kChunksPerRow + ((4 * j + grp) ^ col)];
+#pragma unroll
+    for (int t = 0; t < TW; ++t)
+#pragma unroll
+      for (int m = 0; m < MB; ++m) acc[t][m] = mfma16x16x32(a[m], ring[ks % (D + 1)][t], acc[t][m]);
+    // Phase p+1 goes into the other buffer, last read in phase p-1, which
+    // every wave left at the previous barrier; one barrier per phase.
+    if (NP > 1 && p + 1 < NP && j == KP - 1) {
+      store_a((p + 1) & 1);
+      __syncthreads();
+    }
+  }
+  // Epilogue: bf16 logits, optional store, running best per row over this
+  // lane's columns (ascending index, strict compare keeps the first).
+  uint32_t bk[MB][4];
+  int bi[MB][4];
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bk[m][i] = 0u;
+      bi[m][i] = vocab;
+    }
+#pragma unroll
+  for (int t = 0; t < TW; ++t) {
+    const int v = (tile0 + t) * 16 + col;
+    const bool in = v < vocab;
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t h = f32_to_bf16(acc[t][m][i]);
+        const int row = m * 16 + grp * 4 + i;
+        if (logits && in && row < M) logits[(int64_t)row * ldo + v] = (bf16)h;
+        const uint32_t key1 = order_key(f32_to_bf16(bf16_to_f32(h) * inv_scaling)) + 1u;
+        if (in && key1 > bk[m][i]) {
+          bk[m][i] = key1;
+          bi[m][i] = v;
+        }
+      }
+  }
+  // Largest word over the 16 lanes of each row group, then over the waves.
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint64_t b = bk[m][i] ? pack_best(bk[m][i], bi[m][i]) : 0ull;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)b, off, kWave);
+        const uint32_t hi = __shfl_xor((uint32_t)(b >> 32), off, kWave);
+        b = max_u64(b, ((uint64_t)hi << 32) | lo);
+      }
+      if (col == 0) wbest[wave][m * 16 + grp * 4 + i] = b;
+    }
+  __syncthreads();
+  for (int row = threadIdx.x; row < M; row += kHeadThreads) {
+    uint64_t b = wbest[0][row];
+#pragma unroll
+    for (int w = 1; w < kHeadWaves; ++w) b = max_u64(b, wbest[w][row]);
+    best_out[(int64_t)row * gridDim.x + blockIdx.x] = b;
+  }
+}
+
+int head_row_blocks(int64_t rows) { return rows <= 16 ? 1 : rows <= 32 ? 2 : rows <= 64 ? 4 : 8; }
+
+// Workgroups of the fused head: one per slice of 4*TW vocabulary tiles.
+int64_t head_parts(int64_t rows, int64_t vocab) {
+  const int mb = head_row_blocks(rows);
+  const int tw = mb <= 4 ? head_tiles_per_wave<4>() : head_tiles_per_wave<8>();
+  return cdiv(cdiv(vocab, 16), (int64_t)kHeadWaves * tw);
+}
+
+// The head in MFMA fragment order, k-step major: 16-byte chunk (k-step,
+// tile, lane) = head[16*tile + lane%16][32*k-step + 8*(lane/16) .. +8],
+// zero past the vocabulary (one thread per chunk).
+__global__ void __launch_bounds__(256)
+head_pack_kernel(const bf16 *__restrict__ head, int vocab, int hidden, int64_t chunks,
+                 bf16 *__restrict__ packed) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= chunks) return;
+  const int64_t tiles = cdiv(vocab, 16);
+  const int lane = (int)(q % kWave);
+  const int64_t rest = q / kWave;
+  const int64_t tile = rest % tiles;
+  const int ks = (int)(rest / tiles);
+  const int64_t row = tile * 16 + lane % 16;
+  u32x4 v = u32x4{0u, 0u, 0u, 0u};
+  if (row < vocab) v = load16(head + row * hidden + ks * 32 + (lane / 16) * 8);
+  reinterpret_cast<u32x4 *>(packed)[q] = v;
+}
+
+bool head_shape_ok(int64_t rows, int64_t vocab, int64_t hidden) {
+  if (rows < 1 || rows > 128 || vocab < 1 || vocab >= ((int64_t)1 << 31)) return false;
+  return hidden == 512 || hidden == 1024 || hidden == 1536 || hidden == 2048;
+}
+
 }  // namespace
 }  // namespace lm
 
@@ -303,6 +538,81 @@ extern "C" int lm_greedy_epilogue(const void *logits, int64_t ld, float logits_s
   greedy_update_kernel<<<dim3((unsigned)rows), kWave, 0, s>>>(
       best, parts, valid, next, length, generated, budget, active, emit, eos, (int)neos,
       ignore_eos, emit_ring, ring_depth, step_counter);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+extern "C" int lm_head_greedy_workspace_size(int64_t rows, int64_t vocab, int64_t hidden,
+                                             int64_t *bytes) {
+  LM_REQUIRE(bytes && rows >= 0 && vocab > 0 && hidden > 0);
+  if (rows == 0) {
+    *bytes = 0;
+    return LM_OK;
+  }
+  if (!head_shape_ok(rows, vocab, hidden)) return LM_EUNSUPPORTED;
+  *bytes = rows * head_parts(rows, vocab) * 8;
+  return LM_OK;
+}
+
+extern "C" int lm_head_greedy(const void *z, int64_t ldz, const void *head, int64_t rows,
+                              int64_t vocab, int64_t hidden, float logits_scaling, void *logits,
+                              int64_t ldo, const uint8_t *valid, int64_t *next, int64_t *length,
+                              int64_t *generated, const int64_t *budget, uint8_t *active,
+                              int64_t *emit, const int64_t *eos, int64_t neos, int ignore_eos,
+                              int64_t *emit_ring, int64_t ring_depth, const int64_t *step_counter,
+                              void *workspace, int64_t workspace_bytes, void *stream) {
+  LM_REQUIRE(rows >= 0 && vocab > 0 && hidden > 0 && ldz >= hidden && ldz % 8 == 0 &&
+             (!logits || ldo >= vocab) && neos >= 0 && logits_scaling > 0.f &&
+             (!emit_ring || (ring_depth > 0 && step_counter)));
+  if (rows == 0) return LM_OK;
+  if (!head_shape_ok(rows, vocab, hidden)) return LM_EUNSUPPORTED;
+  LM_REQUIRE(z && head && valid && next && length && generated && budget && active && emit &&
+             (neos == 0 || eos) && workspace);
+  LM_REQUIRE((reinterpret_cast<uintptr_t>(z) & 15) == 0 && (reinterpret_cast<uintptr_t>(head) & 15) == 0);
+  const int64_t parts = head_parts(rows, vocab);
+  if (workspace_bytes < rows * parts * 8) return LM_EWORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  uint64_t *best = static_cast<uint64_t *>(workspace);
+  const float inv = 1.0f / logits_scaling;
+  const int mb = head_row_blocks(rows);
+  const dim3 grid((unsigned)parts);
+  bool launched = false;
+#define LM_HEAD(MB, KS)                                                                          \
+  if (!launched && mb == MB && hidden == KS * 32) {                                              \
+    head_argmax_kernel<MB, KS><<<grid, kHeadThreads, 0, s>>>(                                    \
+        (const bf16 *)z, ldz, (const bf16 *)head, (int)rows, (int)vocab, inv, (bf16 *)logits,   \
+        ldo, best);                                                                              \
+    launched = true;                                                                             \
+  }
+#define LM_HEAD_KS(MB) LM_HEAD(MB, 16) LM_HEAD(MB, 32) LM_HEAD(MB, 48) LM_HEAD(MB, 64)
+  LM_HEAD_KS(1) LM_HEAD_KS(2) LM_HEAD_KS(4) LM_HEAD_KS(8)
+#undef LM_HEAD_KS
+#undef LM_HEAD
+  if (!launched) return LM_EUNSUPPORTED;
+  LM_CHECK_LAUNCH();
+  greedy_update_kernel<<<dim3((unsigned)rows), kWave, 0, s>>>(
+      best, (int)parts, valid, next, length, generated, budget, active, emit, eos, (int)neos,
+      ignore_eos, emit_ring, ring_depth, step_counter);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+extern "C" int lm_head_pack_size(int64_t vocab, int64_t hidden, int64_t *bytes) {
+  LM_REQUIRE(bytes && vocab > 0 && hidden > 0);
+  if (hidden % 32) return LM_EUNSUPPORTED;
+  *bytes = cdiv(vocab, 16) * 16 * hidden * 2;
+  return LM_OK;
+}
+
+extern "C" int lm_head_pack(const void *head, int64_t vocab, int64_t hidden, void *packed,
+                            void *stream) {
+  LM_REQUIRE(head && packed && vocab > 0 && vocab < ((int64_t)1 << 31) && hidden > 0);
+  if (hidden % 32) return LM_EUNSUPPORTED;
+  LM_REQUIRE((reinterpret_cast<uintptr_t>(head) & 15) == 0 &&
+             (reinterpret_cast<uintptr_t>(packed) & 15) == 0);
+  const int64_t chunks = cdiv(vocab, 16) * 16 * hidden / 8;
+  head_pack_kernel<<<dim3((unsigned)cdiv(chunks, 256)), 256, 0, (hipStream_t)stream>>>(
+      (const bf16 *)head, (int)vocab, (int)hidden, chunks, (bf16 *)packed);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

@@ -39,7 +39,7 @@ from .rope import rope_kv_write
 from .router import add_rmsnorm_route as route_add_rmsnorm
 from .router import add_rmsnorm_route_splitk as route_add_rmsnorm_splitk
 from .router import route
-from .step import decode_prologue, greedy_epilogue
+from .step import PackedHead, decode_prologue, greedy_epilogue, greedy_head, head_supported
 
 
 class Granite:
@@ -51,6 +51,7 @@ class Granite:
         self.decode_lean = False   # positions pre-zeroed for stopped rows; outputs unmasked
         self.used = None
         self._row_order = None     # the decode prologue's row order, during greedy_step only
+        self.fused_head = True     # greedy_step: LM head with the argmax in its epilogue (lm_head_greedy)
         self._flash = {}
         device, dtype = weights["embedding"].device, weights["embedding"].dtype
         dim = cfg.hidden_size // cfg.num_attention_heads
@@ -62,6 +63,11 @@ class Granite:
         self.cos_sin = torch.cat((freq.cos(), freq.sin()), -1).to(dtype)
         self.cos, self.sin = [half.repeat(1, 2) for half in self.cos_sin.chunk(2, -1)]
         self.prepare_packed_qkv()
+        # The head in the fused greedy head's fragment order (a second copy,
+        # made once; the embedding keeps the checkpoint layout).
+        head = weights["head"]
+        self.packed_head = (PackedHead(head) if head.is_cuda and head.is_contiguous() and
+                            head_supported(1, head.shape[0], cfg.hidden_size) else None)
 
     def prepare_packed_qkv(self):
         for w in self.w["layers"]:
@@ -189,8 +195,14 @@ class Granite:
             z = self._fused_layers(x, z, cache, positions, valid, positions, None)
         finally:
             self._row_order = None
-        greedy_epilogue(F.linear(z, self.w["head"]), cfg.logits_scaling, valid, state, emit, eos,
-                        ignore_eos, ring_target=target)
+        head = self.w["head"]
+        if self.fused_head and self.packed_head is not None and head_supported(rows, head.shape[0],
+                                                                               cfg.hidden_size):
+            greedy_head(z, self.packed_head, cfg.logits_scaling, valid, state, emit, eos, ignore_eos,
+                        ring_target=target)
+        else:
+            greedy_epilogue(F.linear(z, head), cfg.logits_scaling, valid, state, emit, eos,
+                            ignore_eos, ring_target=target)
 
     def forward(self, tokens, positions, valid, cache, slot=None, last=None, communication_tokens=None):
         cfg = self.cfg

@@ -7,6 +7,9 @@ replaces the logits scaling and everything after the forward
 (model.py:127, engine.py:92-102): the argmax, the emit row and the state
 update. Both keep the reference's arithmetic, so a step through them emits
 the same tokens and leaves the same state as the reference's torch ops.
+``greedy_head`` folds the LM head product into the epilogue: the head
+weights are streamed once with the argmax in the product's epilogue, and
+the logits are not materialised unless asked for.
 """
 import torch
 
@@ -91,3 +94,64 @@ def greedy_epilogue(logits, logits_scaling, valid, state, emit, eos, ignore_eos,
               _bool_bytes(state["active"]).data_ptr(), emit.data_ptr(),
               eos.data_ptr() if eos.numel() else None, eos.numel(), int(bool(ignore_eos)),
               ring_ptr, depth, _lib.ptr(counter), ws.data_ptr(), ws.numel(), _lib.stream(logits.device))
+
+
+def head_supported(rows, vocab, hidden):
+    """Whether :func:`greedy_head` has a kernel for this shape (rows <= 128,
+    hidden 512/1024/1536/2048)."""
+    return 1 <= rows <= 128 and 0 < vocab < 2 ** 31 and hidden in (512, 1024, 1536, 2048)
+
+
+class PackedHead:
+    """The LM head ``[vocab, hidden]`` in MFMA fragment order
+    (``lm_head_pack``): what :func:`greedy_head` streams."""
+
+    def __init__(self, head):
+        _lib.require_cuda(head, what="head")
+        if head.dtype != torch.bfloat16 or head.dim() != 2 or not head.is_contiguous():
+            raise ValueError("head must be a contiguous bf16 [vocab, hidden] tensor")
+        self.vocab, self.hidden = head.shape
+        nbytes = _lib.size_query("lm_head_pack_size", self.vocab, self.hidden)
+        self.packed = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=head.device)
+        _lib.call("lm_head_pack", head.data_ptr(), self.vocab, self.hidden, self.packed.data_ptr(),
+                  _lib.stream(head.device))
+
+
+def greedy_head(z, head, logits_scaling, valid, state, emit, eos, ignore_eos, ring_target=None,
+                logits_out=None):
+    """The LM head product and :func:`greedy_epilogue` in two launches: the
+    packed head (:class:`PackedHead`) is streamed once with the argmax in the
+    product's epilogue, then the state update. Same candidate, emit rows and
+    state as ``greedy_epilogue(F.linear(z, head), ...)`` given the same bf16
+    logits; ``logits_out`` (bf16 ``[rows, vocab]``, optional) receives them
+    (litemoe/model.py:127 and litemoe/engine.py:92-102)."""
+    _lib.require_cuda(z, head.packed, valid, emit, eos, what="greedy head inputs")
+    rows, hidden = z.shape
+    vocab = head.vocab
+    if z.dtype != torch.bfloat16:
+        raise ValueError("z must be bf16")
+    if z.stride(1) != 1 or head.hidden != hidden:
+        raise ValueError("z must have unit column stride and the head's hidden size")
+    if not head_supported(rows, vocab, hidden):
+        raise ValueError(f"no fused head kernel for rows={rows}, hidden={hidden}")
+    for name in ("next", "length", "generated", "budget"):
+        t = state[name]
+        if t.dtype != torch.int64 or not t.is_contiguous() or t.shape != (rows,):
+            raise ValueError(f"state[{name!r}] must be contiguous int64 [rows]")
+    if emit.dtype != torch.int64 or emit.shape != (rows, 3) or not emit.is_contiguous():
+        raise ValueError("emit must be contiguous int64 [rows, 3]")
+    if eos.dtype != torch.int64 or not eos.is_contiguous():
+        raise ValueError("eos must be a contiguous int64 tensor")
+    if logits_out is not None and (logits_out.dtype != torch.bfloat16 or logits_out.shape != (rows, vocab)
+                                   or logits_out.stride(1) != 1):
+        raise ValueError("logits_out must be bf16 [rows, vocab] with unit column stride")
+    ring_ptr, depth, counter = (None, 0, None) if ring_target is None else ring_target
+    nbytes = _lib.size_query("lm_head_greedy_workspace_size", rows, vocab, hidden)
+    ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=z.device)
+    _lib.call("lm_head_greedy", z.data_ptr(), z.stride(0), head.packed.data_ptr(), rows, vocab, hidden,
+              float(logits_scaling), _lib.ptr(logits_out), 0 if logits_out is None else logits_out.stride(0),
+              _bool_bytes(valid).data_ptr(), state["next"].data_ptr(), state["length"].data_ptr(),
+              state["generated"].data_ptr(), state["budget"].data_ptr(),
+              _bool_bytes(state["active"]).data_ptr(), emit.data_ptr(),
+              eos.data_ptr() if eos.numel() else None, eos.numel(), int(bool(ignore_eos)),
+              ring_ptr, depth, _lib.ptr(counter), ws.data_ptr(), ws.numel(), _lib.stream(z.device))

@@ -40,6 +40,9 @@ def test_workspace_queries():
     assert _lib.size_query("lm_flash_decode_workspace_size", 64, 24, 64, 1) == 0
     n = 64 * 24 * 5
     assert _lib.size_query("lm_flash_decode_workspace_size", 64, 24, 64, 5) == n * 256 + 2 * n * 4
+    # fused head: one 8-byte argmax word per row and slice of 12 vocabulary tiles (8 above 64 rows)
+    assert _lib.size_query("lm_head_greedy_workspace_size", 64, 49155, 1536) == 64 * 257 * 8
+    assert _lib.size_query("lm_head_greedy_workspace_size", 128, 49155, 1536) == 128 * 385 * 8
 
 
 @pytest.mark.parametrize("call,expected", [
@@ -82,6 +85,21 @@ _P = 16
     ("flash workspace short", lambda h: h.lm_flash_decode(_P, 64 * 24, 64, _P, _P, _P, 64, 24, 8, 2048, 64,
                                                             C.c_float(0.125), 2048, 4, _P, _P, 16, None), 4),
     ("finish topk 9", lambda h: h.lm_moe_finish(_P, _P, None, _P, None, _P, 1, 8, 9, 0, 1, None, 0, None), 1),
+    ("head rows 129", lambda h: h.lm_head_greedy(_P, 1536, _P, 129, 49155, 1536, C.c_float(8.0), None, 0, _P, _P,
+                                                   _P, _P, _P, _P, _P, None, 0, 1, None, 0, None, _P, 1 << 30, None),
+     2),
+    ("head hidden 1000", lambda h: h.lm_head_greedy(_P, 1000, _P, 64, 49155, 1000, C.c_float(8.0), None, 0, _P,
+                                                      _P, _P, _P, _P, _P, _P, None, 0, 1, None, 0, None, _P, 1 << 30,
+                                                      None), 2),
+    ("head workspace short", lambda h: h.lm_head_greedy(_P, 1536, _P, 64, 49155, 1536, C.c_float(8.0), None, 0,
+                                                          _P, _P, _P, _P, _P, _P, _P, None, 0, 1, None, 0, None, _P,
+                                                          64 * 8, None), 4),
+    ("head z misaligned", lambda h: h.lm_head_greedy(_P + 2, 1536, _P, 64, 49155, 1536, C.c_float(8.0), None, 0,
+                                                       _P, _P, _P, _P, _P, _P, _P, None, 0, 1, None, 0, None, _P,
+                                                       1 << 30, None), 1),
+    ("head scaling 0", lambda h: h.lm_head_greedy(_P, 1536, _P, 64, 49155, 1536, C.c_float(0.0), None, 0, _P, _P,
+                                                    _P, _P, _P, _P, _P, None, 0, 1, None, 0, None, _P, 1 << 30, None),
+     1),
     ("ok: zero tokens", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 0, 1024, 512, 8, 2, 0, _P, _P, 0,
                                                        None), 0),
 ])

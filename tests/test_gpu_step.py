@@ -205,6 +205,7 @@ def test_lean_greedy_step_equals_forward_step(hidden):
         run.prefill()
     assert torch.equal(runs[0].cache.k, runs[1].cache.k)
     supported = model.greedy_supported
+    model.fused_head = False  # the head product as forward computes it (F.linear), for bitwise equality
     for _ in range(8):
         runs[0].decode_step()
         model.greedy_supported = lambda: False
@@ -219,3 +220,99 @@ def test_lean_greedy_step_equals_forward_step(hidden):
         assert torch.equal(runs[0].cache.v, runs[1].cache.v)
     with optimized_policy(runs[0]):
         assert model.greedy_supported()
+
+
+@pytest.mark.parametrize("rows,vocab,hidden", [(64, 49155, 1536), (32, 49155, 1024), (128, 5003, 1536),
+                                               (1, 97, 512), (17, 1000, 2048), (100, 777, 1024),
+                                               (48, 16, 1536)])
+@pytest.mark.parametrize("ignore_eos", [False, True])
+@torch.inference_mode()
+def test_head_greedy_equals_epilogue_on_its_logits(rows, vocab, hidden, ignore_eos):
+    """lm_head_greedy against lm_greedy_epilogue (itself bit-exact against the
+    reference's torch step) on the logits the fused head computes: the same
+    candidates, emit rows and state bit for bit, with or without the logits
+    stored. The logits against an fp32 product of the same bf16 operands:
+    within one bf16 rounding (rtol 2^-7, atol 1e-3), rel-L2 <= 2e-2 as the
+    north-star bar; the candidate is a maximum of the fp32 product's scaled
+    values up to one bf16 ulp (the argmax of a different BLAS order may pick
+    another index among near-ties, so agreement is reported, not required)."""
+    seed = rows * 3 + vocab + hidden
+    scaling = 8.0
+    z = normal_bf16((rows, hidden), 1.0, seed).to(DEV)
+    head = normal_bf16((vocab, hidden), 0.02, seed + 1)
+    g = torch.Generator().manual_seed(seed)
+    # planted ties: copies of one head row give equal logits at several indices
+    for _ in range(4):
+        src, dst = torch.randint(0, vocab, (2,), generator=g).tolist()
+        head[dst] = head[src]
+    head = head.to(DEV)
+    s = state_for(rows, vocab, seed)
+    valid = s["active"].clone()
+    eos = torch.tensor([3, 11], dtype=torch.int64, device=DEV)
+    logits = torch.full((rows, vocab), float("nan"), dtype=torch.bfloat16, device=DEV)
+    got_s = {k: v.clone() for k, v in s.items()}
+    exp_s = {k: v.clone() for k, v in s.items()}
+    bare_s = {k: v.clone() for k, v in s.items()}
+    got_emit = torch.full((rows, 3), -5, dtype=torch.int64, device=DEV)
+    exp_emit, bare_emit = got_emit.clone(), got_emit.clone()
+    packed = step.PackedHead(head)
+    step.greedy_head(z, packed, scaling, valid, got_s, got_emit, eos, ignore_eos, logits_out=logits)
+    step.greedy_epilogue(logits, scaling, valid, exp_s, exp_emit, eos, ignore_eos)
+    step.greedy_head(z, packed, scaling, valid, bare_s, bare_emit, eos, ignore_eos)
+    assert torch.equal(got_emit, exp_emit)
+    assert torch.equal(bare_emit, exp_emit)
+    for k in s:
+        assert torch.equal(got_s[k], exp_s[k]), k
+        assert torch.equal(bare_s[k], exp_s[k]), k
+    ref = z.float() @ head.float().T
+    got = logits.float()
+    assert torch.allclose(got, ref, rtol=2 ** -7, atol=1e-3)
+    assert float((got - ref).norm() / ref.norm()) <= 2e-2
+    scaled = (ref.to(torch.bfloat16) / scaling).float()
+    cand = got_emit[:, 0]
+    picked = scaled.gather(1, cand[:, None])[:, 0]
+    top = scaled.max(-1).values
+    assert bool((picked >= top - top.abs() * 2 ** -6 - 1e-6).all())  # two bf16 roundings apart
+    agree = int((cand == scaled.argmax(-1)).sum())
+    print(f"head argmax agreement with the fp32 product: {agree}/{rows}")
+
+
+@torch.inference_mode()
+def test_head_greedy_ring_and_limits():
+    """The emit ring slot written by the fused head path equals the emit
+    rows; shapes without a kernel raise."""
+    rows, vocab, hidden = 8, 300, 512
+    z = normal_bf16((rows, hidden), 1.0, 1).to(DEV)
+    head = normal_bf16((vocab, hidden), 0.02, 2).to(DEV)
+    s = state_for(rows, vocab, 5)
+    valid = s["active"].clone()
+    eos = torch.zeros(0, dtype=torch.int64, device=DEV)
+    emit = torch.zeros(rows, 3, dtype=torch.int64, device=DEV)
+    host = torch.full((2, rows, 3), -1, dtype=torch.int64, pin_memory=True)
+    import ctypes
+    address = ctypes.c_void_p()
+    _lib.call("lm_host_device_pointer", host.data_ptr(), ctypes.byref(address))
+    counter = torch.full((1,), 2, dtype=torch.int64, device=DEV)  # step 2 -> slot 1
+    step.greedy_head(z, step.PackedHead(head), 4.0, valid, s, emit, eos, True,
+                     ring_target=(address.value, 2, counter))
+    torch.cuda.synchronize()
+    assert torch.equal(host[1], emit.cpu())
+    assert bool((host[0] == -1).all())
+    with pytest.raises(ValueError):
+        step.greedy_head(z[:, :256].contiguous(), step.PackedHead(head[:, :256].contiguous()), 4.0, valid, s,
+                         emit, eos, True)
+    with pytest.raises(_lib.NativeError):
+        nbytes = ctypes.c_int64()
+        _lib.call("lm_head_greedy_workspace_size", 129, vocab, hidden, ctypes.byref(nbytes))
+
+
+@torch.inference_mode()
+def test_head_pack_layout():
+    """lm_head_pack's chunk (k, tile, lane) is head[16*tile + lane%16][32*k + 8*(lane/16) .. +8], zero past
+    the vocabulary."""
+    vocab, hidden = 37, 512
+    head = normal_bf16((vocab, hidden), 1.0, 3).to(DEV)
+    packed = step.PackedHead(head).packed.view(hidden // 32, 3, 64, 8).cpu()
+    h = torch.cat([head.cpu(), torch.zeros(48 - vocab, hidden, dtype=torch.bfloat16)])
+    expect = h.view(3, 16, hidden // 32, 4, 8).permute(2, 0, 3, 1, 4).reshape(hidden // 32, 3, 64, 8)
+    assert torch.equal(packed, expect)
