@@ -108,14 +108,20 @@ def moe_roofline(model, cfg, batch, reps):
     stream = _lib.stream(dev)
     out = torch.empty(batch, H, device=dev, dtype=torch.bfloat16)
 
+    # the weights the decode step reads: the fragment layout when the model packed them
+    packed = "input_linear_packed" in model.w["layers"][0]
+    w13_key, w2_key = ("input_linear_packed", "output_linear_packed") if packed else ("input_linear",
+                                                                                      "output_linear")
+
     def gate_up_all():  # the decode path: each expert's workgroups collect its routes
         for w, weights, ids, offsets, order, act, _ in per_layer:
-            _lib.call("lm_moe_gate_up", z.data_ptr(), w["input_linear"].data_ptr(), None, None,
-                      ids.data_ptr(), batch * k, k, H, I, E, 0, act.data_ptr(), stream)
+            _lib.call("lm_moe_gate_up_packed" if packed else "lm_moe_gate_up", z.data_ptr(),
+                      w[w13_key].data_ptr(), None, None, ids.data_ptr(), batch * k, k, H, I, E, 0,
+                      act.data_ptr(), stream)
 
     def fused_all():
         for w, weights, ids, *_ in per_layer:
-            experts.fused_experts(z, w["input_linear"], w["output_linear"], weights, ids, out=out)
+            experts.fused_experts(z, w[w13_key], w[w2_key], weights, ids, out=out, packed=packed)
 
     result = {}
     for name, fn in (("gate_up", gate_up_all), ("fused", fused_all)):

@@ -401,6 +401,51 @@ int lm_moe_routes(const void *x, const void *w13, const void *w2,
                   int64_t block_rows, void *y, void *workspace,
                   int64_t workspace_bytes, void *stream);
 
+/* Expert weights in MFMA fragment order, done once when the model is
+ * loaded (two launches): for each matrix M [rows][K] (w13 as
+ * [experts*2*inter][hidden], w2 as [experts*hidden][inter]), 16-byte chunk
+ * (tile, k, lane) of the packed copy = M[16*tile + lane%16][32*k +
+ * 8*(lane/16) .. +8], tiles of 16 rows, k-steps of 32. Every MFMA weight
+ * fragment a kernel loads (16 rows x 32 k, one per lane) is then 1 KB
+ * contiguous, and a decode workgroup's weight tile one contiguous run.
+ * Same sizes as the inputs; hidden and inter as lm_fused_experts requires;
+ * all four pointers 16-byte aligned; no aliasing. Replaces the reference's
+ * load-time weight preparation (litemoe/weights.py:80-108, model.py:37-40),
+ * which keeps the checkpoint layout for vLLM. */
+int lm_expert_pack(const void *w13, const void *w2, int64_t experts,
+                   int64_t hidden, int64_t inter, void *w13_packed,
+                   void *w2_packed, void *stream);
+
+/* lm_moe_gate_up, lm_moe_down, lm_moe_routes and lm_fused_experts on
+ * weights packed by lm_expert_pack: the same arguments, kernels, arithmetic
+ * order and results bit for bit. */
+int lm_moe_gate_up_packed(const void *x, const void *w13,
+                          const int32_t *expert_offsets,
+                          const int32_t *sorted_routes,
+                          const int32_t *topk_ids, int64_t routes,
+                          int64_t topk, int64_t hidden, int64_t inter,
+                          int64_t experts, int64_t block_rows, void *act,
+                          void *stream);
+int lm_moe_down_packed(const void *act, const void *w2,
+                       const int32_t *expert_offsets,
+                       const int32_t *sorted_routes, const int32_t *topk_ids,
+                       int64_t routes, int64_t hidden, int64_t inter,
+                       int64_t experts, int64_t block_rows, void *y,
+                       void *stream);
+int lm_moe_routes_packed(const void *x, const void *w13, const void *w2,
+                         const int32_t *topk_ids, int64_t tokens,
+                         int64_t hidden, int64_t inter, int64_t experts,
+                         int64_t topk, int64_t block_rows, void *y,
+                         void *workspace, int64_t workspace_bytes,
+                         void *stream);
+int lm_fused_experts_packed(const void *x, const void *w13, const void *w2,
+                            const float *topk_weights,
+                            const int32_t *topk_ids, const int64_t *logical,
+                            int64_t tokens, int64_t hidden, int64_t inter,
+                            int64_t experts, int64_t topk, int64_t block_rows,
+                            void *out, void *workspace,
+                            int64_t workspace_bytes, void *stream);
+
 /* The combine of lm_moe_finish (y in route order, all routes owned) fused
  * with the residual add and the next RMSNorm:
  *   m[t] = bf16(finish(y, ids, scales)[t]);  x[t] <- bf16(x[t] + alpha*m[t]);

@@ -81,7 +81,10 @@ __device__ __forceinline__ int frag_offset(int row, int chunk) {
 // W13[e, I + j0 + r - kTN/2], output act; otherwise B rows are W2[e, n0 + r],
 // output y. Waves sit in 2 x 2; wave (wr, wc) owns rows wr*kTM/2 .. and, for
 // gate_up, gate and up rows of the same kTN/4 columns j.
-template <bool kGateUp, int kTM, int kTN, int kStages>
+// kPacked: weights in the fragment layout of lm_expert_pack (a load
+// instruction then reads eight whole 128-byte runs: the 8 rows of one
+// (k-step, k-group) are adjacent there).
+template <bool kGateUp, int kTM, int kTN, int kStages, bool kPacked>
 __global__ void __launch_bounds__(kThreads, kTM * kTN > 128 * 128 ? 1 : 4 - kStages)
 expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
                    const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
@@ -124,8 +127,10 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
     const int row = 8 * (wave * kLB + i) + lane / 8;
     const int wrow = kGateUp ? e * 2 * inter + (row < kTN / 2 ? c0 + row : inter + c0 + row - kTN / 2)
                              : e * out_cols + c0 + row;
-    ob[i] = wrow * K + chunk * 8;
+    ob[i] = (int)wofs<kPacked>(wrow, chunk * 8, K);
   }
+  // element advance of one kBK step of B (two 32-wide k-steps when packed)
+  constexpr int kBStep = kPacked ? (int)(kBK / 32 * wstep<true>()) : kBK;
   // One register stage: step k+1 is loaded while step k is computed from
   // LDS, then stored to the other LDS buffer.
   u32x4 ra[kLA], rbv[kLB];
@@ -134,7 +139,7 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
 #pragma unroll
     for (int i = 0; i < kLA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a_src + oa[i] + k0);
 #pragma unroll
-    for (int i = 0; i < kLB; ++i) rbv[i] = *reinterpret_cast<const u32x4 *>(w + ob[i] + k0);
+    for (int i = 0; i < kLB; ++i) rbv[i] = *reinterpret_cast<const u32x4 *>(w + ob[i] + kt * kBStep);
   };
   auto store = [&](int buf) {
     char *base = smem + buf * kStageBytes + lane * 16;
@@ -233,24 +238,33 @@ bool expert_gemm_ok(int64_t routes, int64_t hidden, int64_t inter, int64_t exper
 
 int launch_expert_gemm_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets,
                                const int32_t *sorted, int64_t routes, int64_t topk, int64_t hidden,
-                               int64_t inter, int64_t experts, bf16 *act, hipStream_t stream) {
+                               int64_t inter, int64_t experts, bf16 *act, bool packed,
+                               hipStream_t stream) {
   const int64_t blocks = align_up(cdiv(routes, kTile) + experts, kXcds);
   if (blocks > 65535) return LM_EUNSUPPORTED;
   const dim3 grid((unsigned)(2 * inter / kTile), (unsigned)blocks);
-  expert_gemm_kernel<true, kTile, kTile, kLdsStages><<<grid, kThreads, 0, stream>>>(
-      x, w13, offsets, sorted, (int)topk, (int)hidden, (int)inter, (int)inter, (int)experts, act);
+  if (packed)
+    expert_gemm_kernel<true, kTile, kTile, kLdsStages, true><<<grid, kThreads, 0, stream>>>(
+        x, w13, offsets, sorted, (int)topk, (int)hidden, (int)inter, (int)inter, (int)experts, act);
+  else
+    expert_gemm_kernel<true, kTile, kTile, kLdsStages, false><<<grid, kThreads, 0, stream>>>(
+        x, w13, offsets, sorted, (int)topk, (int)hidden, (int)inter, (int)inter, (int)experts, act);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }
 
 int launch_expert_gemm_down(const bf16 *act, const bf16 *w2, const int32_t *offsets,
                             const int32_t *sorted, int64_t routes, int64_t hidden, int64_t inter,
-                            int64_t experts, bf16 *y, hipStream_t stream) {
+                            int64_t experts, bf16 *y, bool packed, hipStream_t stream) {
   const int64_t blocks = align_up(cdiv(routes, kTile) + experts, kXcds);
   if (blocks > 65535) return LM_EUNSUPPORTED;
   const dim3 grid((unsigned)(hidden / kTile), (unsigned)blocks);
-  expert_gemm_kernel<false, kTile, kTile, kLdsStages><<<grid, kThreads, 0, stream>>>(
-      act, w2, offsets, sorted, 1, (int)inter, (int)hidden, (int)inter, (int)experts, y);
+  if (packed)
+    expert_gemm_kernel<false, kTile, kTile, kLdsStages, true><<<grid, kThreads, 0, stream>>>(
+        act, w2, offsets, sorted, 1, (int)inter, (int)hidden, (int)inter, (int)experts, y);
+  else
+    expert_gemm_kernel<false, kTile, kTile, kLdsStages, false><<<grid, kThreads, 0, stream>>>(
+        act, w2, offsets, sorted, 1, (int)inter, (int)hidden, (int)inter, (int)experts, y);
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

@@ -130,7 +130,7 @@ struct RouteSet {
 
 // KS: 32-wide k steps per wave, hidden = KS * 32 * kWaves. Column tile of 16
 // gate rows and the matching 16 up rows.
-template <int KS, int kMode>
+template <int KS, int kMode, bool kPacked>
 __global__ void __launch_bounds__(kThreads)
 gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
                const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
@@ -146,12 +146,13 @@ gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
   const int kbase = wave * KS * 32 + grp * 8;
   u32x4 bg[KS], bu[KS];
   auto load_weights = [&](int e) {
-    const bf16 *wg = w13 + ((int64_t)e * 2 * inter + n0 + col) * hidden + kbase;
-    const bf16 *wu = wg + (int64_t)inter * hidden;
+    const int64_t rg = (int64_t)e * 2 * inter + n0 + col;
+    const bf16 *wg = w13 + wofs<kPacked>(rg, kbase, hidden);
+    const bf16 *wu = w13 + wofs<kPacked>(rg + inter, kbase, hidden);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      bg[s] = load16(wg + s * 32);
-      bu[s] = load16(wu + s * 32);
+      bg[s] = load16(wg + s * wstep<kPacked>());
+      bu[s] = load16(wu + s * wstep<kPacked>());
     }
   };
   RouteSet set{sorted, nullptr, 0, 0};
@@ -223,7 +224,7 @@ gate_up_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
 // runs without the row-block loop. That keeps a wave within 128 registers up
 // to hidden 1536, so four workgroups share a CU: 1024 of the decode step's
 // 1280 weight tiles (Granite-3B shape) are in flight at once instead of 768.
-template <int KS>
+template <int KS, bool kPacked>
 __global__ void __launch_bounds__(kThreads, KS <= 12 ? 4 : 2)
 gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
                     const int32_t *__restrict__ ids, int routes, int topk, int hidden, int inter,
@@ -235,15 +236,16 @@ gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
   const int col = lane % 16, grp = lane / 16;
   const int e = blockIdx.y, n0 = blockIdx.x * 16;
   const int kbase = wave * KS * 32 + grp * 8;
-  const bf16 *wg = w13 + ((int64_t)e * 2 * inter + n0 + col) * hidden + kbase;
-  const bf16 *wu = wg + (int64_t)inter * hidden;
+  const int64_t rg = (int64_t)e * 2 * inter + n0 + col;
+  const bf16 *wg = w13 + wofs<kPacked>(rg, kbase, hidden);
+  const bf16 *wu = w13 + wofs<kPacked>(rg + inter, kbase, hidden);
   u32x4 bg[KS], bu[KS], a[KS];
   const ScanIds scan = load_ids(ids, routes);
   __builtin_amdgcn_sched_barrier(0);  // ids first: the scan waits for them only
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    bg[s] = load16(wg + s * 32);
-    bu[s] = load16(wu + s * 32);
+    bg[s] = load16(wg + s * wstep<kPacked>());
+    bu[s] = load16(wu + s * wstep<kPacked>());
   }
   __builtin_amdgcn_sched_barrier(0);
   const int n = scan_ids(scan, e, list, wave_count);
@@ -287,7 +289,7 @@ gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
 
 // KS: 32-wide k steps per wave, inter = KS * 32 * kWaves. Column tile of 32
 // (two MFMA tiles).
-template <int KS, int kMode>
+template <int KS, int kMode, bool kPacked>
 __global__ void __launch_bounds__(kThreads)
 down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
             const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
@@ -303,12 +305,13 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
   const int kbase = wave * KS * 32 + grp * 8;
   u32x4 b0[KS], b1[KS];
   auto load_weights = [&](int e) {
-    const bf16 *w0 = w2 + ((int64_t)e * hidden + n0 + col) * inter + kbase;
-    const bf16 *w1 = w0 + (int64_t)16 * inter;
+    const int64_t r0 = (int64_t)e * hidden + n0 + col;
+    const bf16 *w0 = w2 + wofs<kPacked>(r0, kbase, inter);
+    const bf16 *w1 = w2 + wofs<kPacked>(r0 + 16, kbase, inter);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      b0[s] = load16(w0 + s * 32);
-      b1[s] = load16(w1 + s * 32);
+      b0[s] = load16(w0 + s * wstep<kPacked>());
+      b1[s] = load16(w1 + s * wstep<kPacked>());
     }
   };
   RouteSet set{sorted, nullptr, 0, 0};
@@ -380,7 +383,7 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
 // per wave, inter = KS * 32 * kWaves); its activation loads are issued back
 // to back. Same MFMA order and wave-order sum as down_kernel, hence the same
 // bits.
-template <int KS, int NT>
+template <int KS, int NT, bool kPacked>
 __global__ void __launch_bounds__(kThreads)
 down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
                  const int32_t *__restrict__ ids, int routes, int hidden, int inter,
@@ -392,14 +395,16 @@ down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
   const int col = lane % 16, grp = lane / 16;
   const int e = blockIdx.y, n0 = blockIdx.x * 16 * NT;
   const int kbase = wave * KS * 32 + grp * 8;
-  const bf16 *w0 = w2 + ((int64_t)e * hidden + n0 + col) * inter + kbase;
+  const int64_t r0 = (int64_t)e * hidden + n0 + col;
   u32x4 b[NT][KS], a[KS];
   const ScanIds scan = load_ids(ids, routes);
   __builtin_amdgcn_sched_barrier(0);  // ids first: the scan waits for them only
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < NT; ++t) {
+    const bf16 *wt = w2 + wofs<kPacked>(r0 + 16 * t, kbase, inter);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) b[t][s] = load16(w0 + (int64_t)t * 16 * inter + s * 32);
+    for (int s = 0; s < KS; ++s) b[t][s] = load16(wt + s * wstep<kPacked>());
+  }
   __builtin_amdgcn_sched_barrier(0);
   const int n = scan_ids(scan, e, list, wave_count);
   if (n == 0) return;
@@ -476,9 +481,11 @@ bool scan_path(int64_t tokens, int64_t topk) {
   return tokens <= kMaxScanRows && tokens * topk <= kWaves * kScanIters * kWave;
 }
 
-int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const int32_t *sorted,
-                   const int32_t *ids, int64_t routes, int64_t topk, int64_t hidden, int64_t inter,
-                   int64_t experts, int64_t block_rows, bf16 *act, hipStream_t stream) {
+namespace {
+template <bool kPacked>
+int launch_gate_up_t(const bf16 *x, const bf16 *w13, const int32_t *offsets, const int32_t *sorted,
+                     const int32_t *ids, int64_t routes, int64_t topk, int64_t hidden, int64_t inter,
+                     int64_t experts, int64_t block_rows, bf16 *act, hipStream_t stream) {
   if (routes == 0) return LM_OK;
   const bool scan = ids != nullptr;
   const int bm = (int)block_rows;
@@ -490,13 +497,13 @@ int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const
 #define X(KS)                                                                                   \
   case KS:                                                                                      \
     if (mode == kScanPrefetch)                                                                  \
-      gate_up_scan_kernel<KS><<<grid, kThreads, 0, stream>>>(x, w13, ids, (int)routes,          \
+      gate_up_scan_kernel<KS, kPacked><<<grid, kThreads, 0, stream>>>(x, w13, ids, (int)routes,          \
           (int)topk, (int)hidden, (int)inter, act);                                             \
     else if (mode == kScanLazy)                                                                 \
-      gate_up_kernel<KS, kScanLazy><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted,     \
+      gate_up_kernel<KS, kScanLazy, kPacked><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted,     \
           ids, (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, act);         \
     else                                                                                        \
-      gate_up_kernel<KS, kBlocks><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, ids,  \
+      gate_up_kernel<KS, kBlocks, kPacked><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted, ids,  \
           (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, act);              \
     break;
     LM_KS_LIST(X)
@@ -508,9 +515,10 @@ int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const
   return LM_OK;
 }
 
-int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const int32_t *sorted,
-                const int32_t *ids, int64_t routes, int64_t hidden, int64_t inter, int64_t experts,
-                int64_t block_rows, bf16 *y, hipStream_t stream) {
+template <bool kPacked>
+int launch_down_t(const bf16 *act, const bf16 *w2, const int32_t *offsets, const int32_t *sorted,
+                  const int32_t *ids, int64_t routes, int64_t hidden, int64_t inter, int64_t experts,
+                  int64_t block_rows, bf16 *y, hipStream_t stream) {
   if (routes == 0) return LM_OK;
   const bool scan = ids != nullptr;
   const int bm = (int)block_rows;
@@ -527,7 +535,7 @@ int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const i
     switch (inter / 128) {
 #define X(KS)                                                                                  \
   case KS:                                                                                     \
-    down_scan_kernel<KS, (kNT > 0 ? kNT : 1)><<<sgrid, kThreads, 0, stream>>>(                 \
+    down_scan_kernel<KS, (kNT > 0 ? kNT : 1), kPacked><<<sgrid, kThreads, 0, stream>>>(                 \
         act, w2, ids, (int)routes, (int)hidden, (int)inter, y);                                \
     LM_CHECK_LAUNCH();                                                                         \
     return LM_OK;
@@ -541,13 +549,13 @@ int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const i
 #define X(KS)                                                                                  \
   case KS:                                                                                     \
     if (mode == kScanPrefetch)                                                                 \
-      down_kernel<KS, kScanPrefetch><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted,  \
+      down_kernel<KS, kScanPrefetch, kPacked><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted,  \
           ids, (int)routes, (int)hidden, (int)inter, (int)experts, bm, y);                     \
     else if (mode == kScanLazy)                                                                \
-      down_kernel<KS, kScanLazy><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids, \
+      down_kernel<KS, kScanLazy, kPacked><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids, \
           (int)routes, (int)hidden, (int)inter, (int)experts, bm, y);                          \
     else                                                                                       \
-      down_kernel<KS, kBlocks><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids,   \
+      down_kernel<KS, kBlocks, kPacked><<<grid, kThreads, 0, stream>>>(act, w2, offsets, sorted, ids,   \
           (int)routes, (int)hidden, (int)inter, (int)experts, bm, y);                          \
     break;
     LM_KS_LIST(X)
@@ -557,6 +565,26 @@ int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const i
   }
   LM_CHECK_LAUNCH();
   return LM_OK;
+}
+
+}  // namespace
+
+int launch_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets, const int32_t *sorted,
+                   const int32_t *ids, int64_t routes, int64_t topk, int64_t hidden, int64_t inter,
+                   int64_t experts, int64_t block_rows, bf16 *act, bool packed, hipStream_t stream) {
+  return packed ? launch_gate_up_t<true>(x, w13, offsets, sorted, ids, routes, topk, hidden, inter,
+                                         experts, block_rows, act, stream)
+                : launch_gate_up_t<false>(x, w13, offsets, sorted, ids, routes, topk, hidden, inter,
+                                          experts, block_rows, act, stream);
+}
+
+int launch_down(const bf16 *act, const bf16 *w2, const int32_t *offsets, const int32_t *sorted,
+                const int32_t *ids, int64_t routes, int64_t hidden, int64_t inter, int64_t experts,
+                int64_t block_rows, bf16 *y, bool packed, hipStream_t stream) {
+  return packed ? launch_down_t<true>(act, w2, offsets, sorted, ids, routes, hidden, inter, experts,
+                                      block_rows, y, stream)
+                : launch_down_t<false>(act, w2, offsets, sorted, ids, routes, hidden, inter, experts,
+                                       block_rows, y, stream);
 }
 
 }  // namespace lm
@@ -598,15 +626,15 @@ ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, 
 // act and y in route order.
 int run_routes(const void *x, const void *w13, const void *w2, const int32_t *topk_ids,
                int64_t tokens, int64_t hidden, int64_t inter, int64_t experts, int64_t topk,
-               int64_t block_rows, bf16 *y, const ExpertWorkspace &w, void *stream) {
+               int64_t block_rows, bf16 *y, const ExpertWorkspace &w, bool packed, void *stream) {
   hipStream_t s = (hipStream_t)stream;
   const int64_t routes = tokens * topk;
   if (scan_path(tokens, topk) && block_rows == 0) {
     int rc = launch_gate_up((const bf16 *)x, (const bf16 *)w13, nullptr, nullptr, topk_ids, routes,
-                            topk, hidden, inter, experts, 0, w.act, s);
+                            topk, hidden, inter, experts, 0, w.act, packed, s);
     if (rc) return rc;
     return launch_down(w.act, (const bf16 *)w2, nullptr, nullptr, topk_ids, routes, hidden, inter,
-                       experts, 0, y, s);
+                       experts, 0, y, packed, s);
   }
   const int bm = pick_block_rows(block_rows, tokens);
   int rc = launch_align(topk_ids, routes, 0, experts, w.offsets, w.sorted, nullptr,
@@ -614,16 +642,16 @@ int run_routes(const void *x, const void *w13, const void *w2, const int32_t *to
   if (rc) return rc;
   if (block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts)) {
     rc = launch_expert_gemm_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, routes,
-                                    topk, hidden, inter, experts, w.act, s);
+                                    topk, hidden, inter, experts, w.act, packed, s);
     if (rc) return rc;
     return launch_expert_gemm_down(w.act, (const bf16 *)w2, w.offsets, w.sorted, routes, hidden,
-                                   inter, experts, y, s);
+                                   inter, experts, y, packed, s);
   }
   rc = launch_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, nullptr, routes,
-                      topk, hidden, inter, experts, bm, w.act, s);
+                      topk, hidden, inter, experts, bm, w.act, packed, s);
   if (rc) return rc;
   return launch_down(w.act, (const bf16 *)w2, w.offsets, w.sorted, nullptr, routes, hidden, inter,
-                     experts, bm, y, s);
+                     experts, bm, y, packed, s);
 }
 }  // namespace
 
@@ -641,10 +669,11 @@ extern "C" int lm_moe_routes_workspace_size(int64_t tokens, int64_t topk, int64_
   return LM_OK;
 }
 
-extern "C" int lm_moe_gate_up(const void *x, const void *w13, const int32_t *expert_offsets,
-                              const int32_t *sorted_routes, const int32_t *topk_ids, int64_t routes,
-                              int64_t topk, int64_t hidden, int64_t inter, int64_t experts,
-                              int64_t block_rows, void *act, void *stream) {
+namespace {
+int moe_gate_up(const void *x, const void *w13, const int32_t *expert_offsets,
+                const int32_t *sorted_routes, const int32_t *topk_ids, int64_t routes,
+                int64_t topk, int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
+                void *act, bool packed, void *stream) {
   LM_REQUIRE(routes >= 0 && topk > 0 && experts > 0 && block_rows >= 0 && block_rows % 16 == 0);
   if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
   if (topk_ids && !scan_path(routes / topk, topk)) return LM_EUNSUPPORTED;
@@ -653,16 +682,16 @@ extern "C" int lm_moe_gate_up(const void *x, const void *w13, const int32_t *exp
   if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts))
     return launch_expert_gemm_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets,
                                       sorted_routes, routes, topk, hidden, inter, experts,
-                                      (bf16 *)act, (hipStream_t)stream);
+                                      (bf16 *)act, packed, (hipStream_t)stream);
   return launch_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets, sorted_routes, topk_ids,
                         routes, topk, hidden, inter, experts, pick_block_rows(block_rows, routes),
-                        (bf16 *)act, (hipStream_t)stream);
+                        (bf16 *)act, packed, (hipStream_t)stream);
 }
 
-extern "C" int lm_moe_down(const void *act, const void *w2, const int32_t *expert_offsets,
-                           const int32_t *sorted_routes, const int32_t *topk_ids, int64_t routes,
-                           int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
-                           void *y, void *stream) {
+int moe_down(const void *act, const void *w2, const int32_t *expert_offsets,
+             const int32_t *sorted_routes, const int32_t *topk_ids, int64_t routes, int64_t hidden,
+             int64_t inter, int64_t experts, int64_t block_rows, void *y, bool packed,
+             void *stream) {
   LM_REQUIRE(routes >= 0 && experts > 0 && block_rows >= 0 && block_rows % 16 == 0);
   if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
   if (topk_ids && routes > kWaves * kScanIters * kWave) return LM_EUNSUPPORTED;
@@ -670,17 +699,51 @@ extern "C" int lm_moe_down(const void *act, const void *w2, const int32_t *exper
   LM_REQUIRE(act && w2 && y && (topk_ids || (expert_offsets && sorted_routes)));
   if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts))
     return launch_expert_gemm_down((const bf16 *)act, (const bf16 *)w2, expert_offsets,
-                                   sorted_routes, routes, hidden, inter, experts, (bf16 *)y,
+                                   sorted_routes, routes, hidden, inter, experts, (bf16 *)y, packed,
                                    (hipStream_t)stream);
   return launch_down((const bf16 *)act, (const bf16 *)w2, expert_offsets, sorted_routes, topk_ids,
                      routes, hidden, inter, experts, pick_block_rows(block_rows, routes), (bf16 *)y,
-                     (hipStream_t)stream);
+                     packed, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int lm_moe_gate_up(const void *x, const void *w13, const int32_t *expert_offsets,
+                              const int32_t *sorted_routes, const int32_t *topk_ids, int64_t routes,
+                              int64_t topk, int64_t hidden, int64_t inter, int64_t experts,
+                              int64_t block_rows, void *act, void *stream) {
+  return moe_gate_up(x, w13, expert_offsets, sorted_routes, topk_ids, routes, topk, hidden, inter,
+                     experts, block_rows, act, false, stream);
 }
 
-extern "C" int lm_moe_routes(const void *x, const void *w13, const void *w2,
-                             const int32_t *topk_ids, int64_t tokens, int64_t hidden,
-                             int64_t inter, int64_t experts, int64_t topk, int64_t block_rows,
-                             void *y, void *workspace, int64_t workspace_bytes, void *stream) {
+extern "C" int lm_moe_gate_up_packed(const void *x, const void *w13, const int32_t *expert_offsets,
+                                     const int32_t *sorted_routes, const int32_t *topk_ids,
+                                     int64_t routes, int64_t topk, int64_t hidden, int64_t inter,
+                                     int64_t experts, int64_t block_rows, void *act, void *stream) {
+  return moe_gate_up(x, w13, expert_offsets, sorted_routes, topk_ids, routes, topk, hidden, inter,
+                     experts, block_rows, act, true, stream);
+}
+
+extern "C" int lm_moe_down(const void *act, const void *w2, const int32_t *expert_offsets,
+                           const int32_t *sorted_routes, const int32_t *topk_ids, int64_t routes,
+                           int64_t hidden, int64_t inter, int64_t experts, int64_t block_rows,
+                           void *y, void *stream) {
+  return moe_down(act, w2, expert_offsets, sorted_routes, topk_ids, routes, hidden, inter, experts,
+                  block_rows, y, false, stream);
+}
+
+extern "C" int lm_moe_down_packed(const void *act, const void *w2, const int32_t *expert_offsets,
+                                  const int32_t *sorted_routes, const int32_t *topk_ids,
+                                  int64_t routes, int64_t hidden, int64_t inter, int64_t experts,
+                                  int64_t block_rows, void *y, void *stream) {
+  return moe_down(act, w2, expert_offsets, sorted_routes, topk_ids, routes, hidden, inter, experts,
+                  block_rows, y, true, stream);
+}
+
+namespace {
+int moe_routes(const void *x, const void *w13, const void *w2, const int32_t *topk_ids,
+               int64_t tokens, int64_t hidden, int64_t inter, int64_t experts, int64_t topk,
+               int64_t block_rows, void *y, void *workspace, int64_t workspace_bytes, bool packed,
+               void *stream) {
   LM_REQUIRE(tokens >= 0 && topk > 0 && topk <= experts && block_rows >= 0 &&
              block_rows % 16 == 0 && experts <= 511);
   if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
@@ -689,14 +752,13 @@ extern "C" int lm_moe_routes(const void *x, const void *w13, const void *w2,
   ExpertWorkspace w = carve(workspace, tokens, topk, hidden, inter, experts, false);
   if (workspace_bytes < w.bytes) return LM_EWORKSPACE;
   return run_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows,
-                    (bf16 *)y, w, stream);
+                    (bf16 *)y, w, packed, stream);
 }
 
-extern "C" int lm_fused_experts(const void *x, const void *w13, const void *w2,
-                                const float *topk_weights, const int32_t *topk_ids,
-                                const int64_t *logical, int64_t tokens, int64_t hidden,
-                                int64_t inter, int64_t experts, int64_t topk, int64_t block_rows,
-                                void *out, void *workspace, int64_t workspace_bytes, void *stream) {
+int fused_experts(const void *x, const void *w13, const void *w2, const float *topk_weights,
+                  const int32_t *topk_ids, const int64_t *logical, int64_t tokens, int64_t hidden,
+                  int64_t inter, int64_t experts, int64_t topk, int64_t block_rows, void *out,
+                  void *workspace, int64_t workspace_bytes, bool packed, void *stream) {
   LM_REQUIRE(tokens >= 0 && topk > 0 && topk <= 8 && topk <= experts && block_rows >= 0 &&
              block_rows % 16 == 0 && experts <= 511);
   if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
@@ -705,10 +767,82 @@ extern "C" int lm_fused_experts(const void *x, const void *w13, const void *w2,
   ExpertWorkspace w = carve(workspace, tokens, topk, hidden, inter, experts, true);
   if (workspace_bytes < w.bytes) return LM_EWORKSPACE;
   int rc = run_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows, w.y,
-                      w, stream);
+                      w, packed, stream);
   if (rc) return rc;
   return launch_finish(w.y, topk_ids, nullptr, topk_weights, logical, (bf16 *)out, tokens, hidden,
                        topk, 0, experts, (hipStream_t)stream);
+}
+
+// One thread per 16-byte chunk (tile, k-step, lane) of the fragment layout.
+__global__ void __launch_bounds__(256)
+expert_pack_kernel(const bf16 *__restrict__ src, int K, int64_t chunks, bf16 *__restrict__ dst) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= chunks) return;
+  const int lane = (int)(q % kWave);
+  const int64_t rest = q / kWave;
+  const int steps = K / 32;
+  const int ks = (int)(rest % steps);
+  const int64_t row = (rest / steps) * 16 + lane % 16;
+  reinterpret_cast<u32x4 *>(dst)[q] = load16(src + row * K + ks * 32 + (lane / 16) * 8);
+}
+
+int expert_pack(const void *src, int64_t rows, int64_t K, void *dst, hipStream_t stream) {
+  const int64_t chunks = rows * K / 8;
+  expert_pack_kernel<<<dim3((unsigned)cdiv(chunks, 256)), 256, 0, stream>>>(
+      (const bf16 *)src, (int)K, chunks, (bf16 *)dst);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+}  // namespace
+
+extern "C" int lm_moe_routes(const void *x, const void *w13, const void *w2,
+                             const int32_t *topk_ids, int64_t tokens, int64_t hidden,
+                             int64_t inter, int64_t experts, int64_t topk, int64_t block_rows,
+                             void *y, void *workspace, int64_t workspace_bytes, void *stream) {
+  return moe_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows, y,
+                    workspace, workspace_bytes, false, stream);
+}
+
+extern "C" int lm_moe_routes_packed(const void *x, const void *w13, const void *w2,
+                                    const int32_t *topk_ids, int64_t tokens, int64_t hidden,
+                                    int64_t inter, int64_t experts, int64_t topk,
+                                    int64_t block_rows, void *y, void *workspace,
+                                    int64_t workspace_bytes, void *stream) {
+  return moe_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows, y,
+                    workspace, workspace_bytes, true, stream);
+}
+
+extern "C" int lm_expert_pack(const void *w13, const void *w2, int64_t experts, int64_t hidden,
+                              int64_t inter, void *w13_packed, void *w2_packed, void *stream) {
+  LM_REQUIRE(experts > 0 && hidden > 0 && inter > 0 && w13 && w2 && w13_packed && w2_packed &&
+             w13 != w13_packed && w2 != w2_packed);
+  if (!expert_shapes_ok(hidden, inter)) return LM_EUNSUPPORTED;
+  LM_REQUIRE(((reinterpret_cast<uintptr_t>(w13) | reinterpret_cast<uintptr_t>(w2) |
+               reinterpret_cast<uintptr_t>(w13_packed) | reinterpret_cast<uintptr_t>(w2_packed)) &
+              15) == 0);
+  hipStream_t s = (hipStream_t)stream;
+  const int rc = expert_pack(w13, experts * 2 * inter, hidden, w13_packed, s);
+  if (rc) return rc;
+  return expert_pack(w2, experts * hidden, inter, w2_packed, s);
+}
+
+extern "C" int lm_fused_experts(const void *x, const void *w13, const void *w2,
+                                const float *topk_weights, const int32_t *topk_ids,
+                                const int64_t *logical, int64_t tokens, int64_t hidden,
+                                int64_t inter, int64_t experts, int64_t topk, int64_t block_rows,
+                                void *out, void *workspace, int64_t workspace_bytes, void *stream) {
+  return fused_experts(x, w13, w2, topk_weights, topk_ids, logical, tokens, hidden, inter, experts,
+                       topk, block_rows, out, workspace, workspace_bytes, false, stream);
+}
+
+extern "C" int lm_fused_experts_packed(const void *x, const void *w13, const void *w2,
+                                       const float *topk_weights, const int32_t *topk_ids,
+                                       const int64_t *logical, int64_t tokens, int64_t hidden,
+                                       int64_t inter, int64_t experts, int64_t topk,
+                                       int64_t block_rows, void *out, void *workspace,
+                                       int64_t workspace_bytes, void *stream) {
+  return fused_experts(x, w13, w2, topk_weights, topk_ids, logical, tokens, hidden, inter, experts,
+                       topk, block_rows, out, workspace, workspace_bytes, true, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -771,7 +905,7 @@ extern "C" int lm_fused_experts_noalloc(const void *x, const void *w13, const vo
   if (rc) return rc;
   ExpertWorkspace w = carve(base, tokens, topk, hidden, inter, experts, true);
   const int rr = run_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows,
-                            w.y, w, stream);
+                            w.y, w, false, stream);
   if (rr) return rr;
   return launch_finish(w.y, topk_ids, nullptr, topk_weights, logical, (bf16 *)out, tokens, hidden,
                        topk, 0, experts, (hipStream_t)stream);

@@ -51,8 +51,10 @@ _SHARED = _Workspace()
 
 
 def fused_experts(x, w1, w2, topk_weights, topk_ids, apply_router_weight_on_input=False,
-                  global_num_experts=None, out=None, logical=None, block_rows=0, workspace=None):
-    """``out[t] = sum_j w[t,j] * W2[e] (silu(W13[e,:I] x_t) * W13[e,I:] x_t)``."""
+                  global_num_experts=None, out=None, logical=None, block_rows=0, workspace=None,
+                  packed=False):
+    """``out[t] = sum_j w[t,j] * W2[e] (silu(W13[e,:I] x_t) * W13[e,I:] x_t)``
+    (``packed``: weights from :func:`pack_expert_weights`)."""
     if apply_router_weight_on_input:
         raise ValueError('apply_router_weight_on_input=True is not implemented')
     experts, hidden, inter = _check_weights(x, w1, w2)
@@ -71,7 +73,8 @@ def fused_experts(x, w1, w2, topk_weights, topk_ids, apply_router_weight_on_inpu
     logical64 = logical.to(torch.int64).contiguous() if remap else None
     nbytes = _lib.size_query("lm_fused_experts_workspace_size", tokens, topk, hidden, inter, experts)
     ws = (workspace or _SHARED).get(x.device, nbytes)
-    _lib.call("lm_fused_experts", x.data_ptr(), w1.data_ptr(), w2.data_ptr(), weights.data_ptr(),
+    _lib.call("lm_fused_experts_packed" if packed else "lm_fused_experts", x.data_ptr(), w1.data_ptr(),
+              w2.data_ptr(), weights.data_ptr(),
               ids.data_ptr(), _lib.ptr(logical64), tokens, hidden, inter, experts, topk, block_rows,
               out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(x.device))
     return out
@@ -93,9 +96,11 @@ class HipFusedExperts:
                              global_num_experts, out=out, block_rows=self.block_rows,
                              workspace=self.workspace)
 
-    def routes(self, x, w1, w2, topk_ids):
-        """Unweighted per-route expert outputs ``[M*k, H]`` in route order."""
-        return moe_routes(x, w1, w2, topk_ids, block_rows=self.block_rows, workspace=self.workspace)
+    def routes(self, x, w1, w2, topk_ids, packed=False):
+        """Unweighted per-route expert outputs ``[M*k, H]`` in route order
+        (``packed``: weights from :func:`pack_expert_weights`)."""
+        return moe_routes(x, w1, w2, topk_ids, block_rows=self.block_rows, workspace=self.workspace,
+                          packed=packed)
 
     def __call__(self, x, ids, scales, w1, w2, rank, world, out, logical=None):
         if rank != 0 or world != 1:
@@ -106,9 +111,26 @@ class HipFusedExperts:
                              block_rows=self.block_rows, workspace=self.workspace)
 
 
-def moe_routes(x, w1, w2, topk_ids, block_rows=0, workspace=None, y=None):
+def pack_expert_weights(w1, w2):
+    """The expert weights in MFMA fragment order (``lm_expert_pack``), for
+    the ``packed`` forms of :func:`moe_routes` and :func:`fused_experts`:
+    tensors of the same shapes whose 16-byte chunk (tile, k-step, lane)
+    holds ``M[16*tile + lane%16, 32*k-step + 8*(lane//16):+8]`` of each
+    matrix ``M`` (w1 as ``[E*2I, H]``, w2 as ``[E*H, I]``). Done once at
+    load time; the reference keeps the checkpoint layout for vLLM
+    (litemoe/weights.py:80-108)."""
+    experts, hidden, inter = _check_weights(torch.empty(1, w1.shape[2], dtype=w1.dtype, device=w1.device),
+                                            w1, w2)
+    p1, p2 = torch.empty_like(w1), torch.empty_like(w2)
+    _lib.call("lm_expert_pack", w1.data_ptr(), w2.data_ptr(), experts, hidden, inter, p1.data_ptr(),
+              p2.data_ptr(), _lib.stream(w1.device))
+    return p1, p2
+
+
+def moe_routes(x, w1, w2, topk_ids, block_rows=0, workspace=None, y=None, packed=False):
     """``y[t*k + j] = W2[e] (silu(W13[e,:I] x_t) * W13[e,I:] x_t)`` (bf16
-    roundings as lm_fused_experts), unweighted, in route order."""
+    roundings as lm_fused_experts), unweighted, in route order. ``packed``:
+    w1/w2 come from :func:`pack_expert_weights` (same kernels and results)."""
     experts, hidden, inter = _check_weights(x, w1, w2)
     tokens = x.numel() // hidden
     ids = topk_ids.to(torch.int32).contiguous()
@@ -118,8 +140,9 @@ def moe_routes(x, w1, w2, topk_ids, block_rows=0, workspace=None, y=None):
     y = torch.empty(tokens * topk, hidden, device=x.device, dtype=x.dtype) if y is None else y
     nbytes = _lib.size_query("lm_moe_routes_workspace_size", tokens, topk, hidden, inter, experts)
     ws = (workspace or _SHARED).get(x.device, nbytes)
-    _lib.call("lm_moe_routes", x.data_ptr(), w1.data_ptr(), w2.data_ptr(), ids.data_ptr(), tokens, hidden,
-              inter, experts, topk, block_rows, y.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(x.device))
+    _lib.call("lm_moe_routes_packed" if packed else "lm_moe_routes", x.data_ptr(), w1.data_ptr(), w2.data_ptr(),
+              ids.data_ptr(), tokens, hidden, inter, experts, topk, block_rows, y.data_ptr(), ws.data_ptr(),
+              ws.numel(), _lib.stream(x.device))
     return y
 
 

@@ -31,7 +31,7 @@ import torch.nn.functional as F
 from . import _lib
 from .config import validate_config
 from .flash_decode import FlashDecode
-from .experts import finish_add_rmsnorm
+from .experts import finish_add_rmsnorm, pack_expert_weights
 from .linear import linear_splitk, pick_splits
 from .norm import add_rmsnorm
 from .packed import PackedPrefill, varlen_attention
@@ -63,6 +63,7 @@ class Granite:
         self.cos_sin = torch.cat((freq.cos(), freq.sin()), -1).to(dtype)
         self.cos, self.sin = [half.repeat(1, 2) for half in self.cos_sin.chunk(2, -1)]
         self.prepare_packed_qkv()
+        self.prepare_packed_experts()
         # The head in the fused greedy head's fragment order (a second copy,
         # made once; the embedding keeps the checkpoint layout).
         head = weights["head"]
@@ -73,6 +74,18 @@ class Granite:
         for w in self.w["layers"]:
             if "self_attn.qkv_proj" not in w:
                 w["self_attn.qkv_proj"] = torch.cat([w[f"self_attn.{p}_proj"] for p in ("q", "k", "v")])
+
+    def prepare_packed_experts(self):
+        """Expert weights in MFMA fragment order for the fused layer tail
+        (``lm_expert_pack``), made once next to the checkpoint layout, which
+        the masked expert path keeps using. The fused tail then loads every
+        weight fragment as 1 KB contiguous."""
+        if not getattr(self.ep.backend, "native", False):
+            return
+        for w in self.w["layers"]:
+            w1, w2 = w["input_linear"], w["output_linear"]
+            if "input_linear_packed" not in w and w1.is_cuda and w1.is_contiguous() and w2.is_contiguous():
+                w["input_linear_packed"], w["output_linear_packed"] = pack_expert_weights(w1, w2)
 
     def _decode_attention(self, batch, cache):
         if self.decode_flash is not None:
@@ -159,7 +172,11 @@ class Granite:
                 a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
                 weights, ids, z = route_add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps,
                                                     w["block_sparse_moe.router.layer"], k, z)
-            y = self.ep.backend.routes(z, w["input_linear"], w["output_linear"], ids)
+            if "input_linear_packed" in w:
+                y = self.ep.backend.routes(z, w["input_linear_packed"], w["output_linear_packed"], ids,
+                                           packed=True)
+            else:
+                y = self.ep.backend.routes(z, w["input_linear"], w["output_linear"], ids)
             nxt = layers[layer + 1]["input_layernorm"] if layer + 1 < len(layers) else self.w["norm"]
             finish_add_rmsnorm(y, ids, weights, x, r, nxt, eps, z)
         return z

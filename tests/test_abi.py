@@ -100,6 +100,12 @@ _P = 16
     ("head scaling 0", lambda h: h.lm_head_greedy(_P, 1536, _P, 64, 49155, 1536, C.c_float(0.0), None, 0, _P, _P,
                                                     _P, _P, _P, _P, _P, None, 0, 1, None, 0, None, _P, 1 << 30, None),
      1),
+    ("pack hidden 1000", lambda h: h.lm_expert_pack(_P, _P, 8, 1000, 512, _P + 4096, _P + 8192, None), 2),
+    ("pack aliasing", lambda h: h.lm_expert_pack(_P, _P + 4096, 8, 1024, 512, _P, _P + 8192, None), 1),
+    ("pack misaligned", lambda h: h.lm_expert_pack(_P + 2, _P + 4096, 8, 1024, 512, _P + 8192, _P + 16384, None),
+     1),
+    ("routes packed workspace short", lambda h: h.lm_moe_routes_packed(_P, _P, _P, _P, 64, 1536, 512, 40, 8, 0, _P,
+                                                                         _P, 4096, None), 4),
     ("ok: zero tokens", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 0, 1024, 512, 8, 2, 0, _P, _P, 0,
                                                        None), 0),
 ])

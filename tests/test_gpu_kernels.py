@@ -606,3 +606,59 @@ def test_batched_route_without_norm(renormalize):
     ew, eids = ops.route(logits.cpu(), k, renormalize=renormalize)
     assert torch.equal(ids.cpu(), eids)
     torch.testing.assert_close(weights.cpu(), ew, rtol=2e-6, atol=1e-7)
+
+
+# ----------------------------------------------------- packed expert weights --
+
+@torch.inference_mode()
+def test_expert_pack_layout():
+    """lm_expert_pack's chunk (tile, k, lane) of each matrix M [rows, K] is
+    M[16*tile + lane%16, 32*k + 8*(lane//16):+8] (w1 as [E*2I, H], w2 as [E*H, I])."""
+    e, h, i = 3, 256, 128
+    w1, w2 = bf((e, 2 * i, h), 1.0, 1), bf((e, h, i), 1.0, 2)
+    p1, p2 = experts.pack_expert_weights(w1.to(DEV), w2.to(DEV))
+
+    def expect(m, rows, kk):
+        return m.reshape(rows // 16, 16, kk // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+
+    assert torch.equal(p1.cpu().reshape(-1), expect(w1, e * 2 * i, h))
+    assert torch.equal(p2.cpu().reshape(-1), expect(w2, e * h, i))
+
+
+@pytest.mark.parametrize("m,h,i,e,k,block_rows", [
+    (64, 1536, 512, 40, 8, 0),      # decode scan path (Granite-3B decode)
+    (1, 1536, 512, 40, 8, 0),
+    (32, 1024, 512, 32, 8, 0),      # Granite-1B decode
+    (300, 1024, 512, 32, 8, 0),     # block path (more than 256 tokens)
+    (64, 1536, 512, 40, 8, 16),     # block path forced
+    (640, 1024, 512, 32, 8, 0),     # prefill expert GEMM (>= 4096 routes)
+    (64, 256, 128, 8, 2, 0),
+])
+@torch.inference_mode()
+def test_packed_weights_give_the_same_bits(m, h, i, e, k, block_rows):
+    """Every expert kernel reads the fragment layout to the same bits as the
+    checkpoint layout: the route outputs, the two stages and the fused call."""
+    x, w1, w2, weights, ids = _moe_inputs(m, h, i, e, k, 900 + m + h)
+    xd, w1d, w2d, idsd, wd = (t.to(DEV) for t in (x, w1, w2, ids, weights))
+    p1, p2 = experts.pack_expert_weights(w1d, w2d)
+    ref = experts.moe_routes(xd, w1d, w2d, idsd, block_rows=block_rows)
+    got = experts.moe_routes(xd, p1, p2, idsd, block_rows=block_rows, packed=True)
+    assert torch.equal(got, ref)
+    out_ref = experts.fused_experts(xd, w1d, w2d, wd, idsd, block_rows=block_rows)
+    out = experts.fused_experts(xd, p1, p2, wd, idsd, block_rows=block_rows, packed=True)
+    assert torch.equal(out, out_ref)
+    if m <= 256 and block_rows == 0:
+        # the decode stages on their own, routes collected from topk_ids
+        from litemoe_amd import _lib
+        routes = m * k
+        act = torch.empty(routes, i, device=DEV, dtype=torch.bfloat16)
+        act_ref = experts.gate_up(xd, w1d, None, None, k, topk_ids=idsd.int())
+        _lib.call("lm_moe_gate_up_packed", xd.data_ptr(), p1.data_ptr(), None, None, idsd.int().data_ptr(),
+                  routes, k, h, i, e, 0, act.data_ptr(), _lib.stream(xd.device))
+        assert torch.equal(act, act_ref)
+        y = torch.empty(routes, h, device=DEV, dtype=torch.bfloat16)
+        _lib.call("lm_moe_down_packed", act.data_ptr(), p2.data_ptr(), None, None, idsd.int().data_ptr(),
+                  routes, h, i, e, 0, y.data_ptr(), _lib.stream(xd.device))
+        assert torch.equal(y, ref)
+    if m <= 16:
+        assert rel_l2(got.cpu(), ops.expert_routes(x, ids, w1, w2)) < 1e-2
