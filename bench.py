@@ -69,6 +69,9 @@ def parse():
                     help="skip decode timing: run only the MoE kernel timing (for counter collection)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy a 256 MiB device buffer 3 times (FETCH/WRITE counter calibration)")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="only sum 2048 contiguous 128 KiB rows of a 256 MiB buffer 3 times (a second "
+                         "FETCH_SIZE calibration, in the decode attention's per-row access pattern)")
     ap.add_argument("--prefill", action="store_true", help="cfg 4 packed prefill (own JSON line)")
     ap.add_argument("--flash-decode", action="store_true", help="cfg 5 decode attention (own JSON line)")
     ap.add_argument("--long-decode", action="store_true", help="cfg 5 decode step tok/s (own JSON line)")
@@ -205,9 +208,11 @@ def prefill_bench(args):
         skewed = torch.multinomial(hot.expand(tokens, E), k, replacement=False, generator=rng).int().to(dev)
         moe_flops = tokens * k * 6 * I * H
         moe = {}
+        # the weights the prefill reads (the checkpoint layout; the packed copy serves decode)
+        w13, w2 = layer["input_linear"], layer["output_linear"]
         for name, ids in (("uniform", uniform), ("hot4_50pct", skewed)):
-            y = experts.moe_routes(z, layer["input_linear"], layer["output_linear"], ids)
-            ms = hip_time(lambda: experts.moe_routes(z, layer["input_linear"], layer["output_linear"], ids, y=y), 5)
+            y = experts.moe_routes(z, w13, w2, ids)
+            ms = hip_time(lambda: experts.moe_routes(z, w13, w2, ids, y=y), 5)
             moe[name] = {"ms_per_layer": round(ms, 3), "tflops": round(moe_flops / ms / 1e9, 1),
                          "frac": round(moe_flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
         hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, 64
@@ -443,6 +448,14 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log("copied 3 x 256 MiB")
+        return
+
+    if args.read_probe:
+        a = torch.ones((2048, 65536), dtype=torch.bfloat16, device="cuda")
+        for _ in range(3):
+            a.sum(dim=1)
+        torch.cuda.synchronize()
+        log("read 3 x 256 MiB as 2048 rows of 128 KiB")
         return
 
     if args.prefill:

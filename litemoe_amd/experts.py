@@ -111,6 +111,13 @@ class HipFusedExperts:
                              block_rows=self.block_rows, workspace=self.workspace)
 
 
+def scan_path(tokens, topk):
+    """Whether a call of ``tokens`` rows takes the decode scan path (each
+    expert's workgroups collect their routes from topk_ids): the rule of
+    the library's expert kernels."""
+    return tokens <= 256 and tokens * topk <= 2048
+
+
 def pack_expert_weights(w1, w2):
     """The expert weights in MFMA fragment order (``lm_expert_pack``), for
     the ``packed`` forms of :func:`moe_routes` and :func:`fused_experts`:
