@@ -12,10 +12,13 @@ between device synchronisations (K = 255 covers the whole 256-token
 generation, context 1024 -> 1279). ``value`` = 64 * K / elapsed.
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel (expert gate/up GEMM), timed with HIP
-                events on its stream over all 32 layers' weights (no cache
-                reuse across launches), against 8 TB/s;
-  fused_moe     the whole per-layer MoE (gate_up + down + combine);
+  roofline      the dominant kernel (expert gate/up GEMM on the fragment-order
+                weights), timed with HIP events over all 32 layers' weights
+                (no cache reuse across launches; the 32 launches recorded
+                into a HIP graph and replayed), against 8 TB/s;
+  fused_moe     the whole per-layer MoE as the decode step runs it (expert
+                routes, then combine + residual add + next norm), timed the
+                same way;
   cpu_baseline  the CPU oracle (LiteMoE's torch CPU decode path restated) on a
                 bounded sample of the same decode step, extrapolated;
   engine_decode_tps  the reference's own metric from Engine.generate()
@@ -92,8 +95,11 @@ def measured_traffic(name):
 
 
 def moe_roofline(model, cfg, batch, reps):
-    """Time the gate/up kernel and the whole fused MoE per layer with HIP
-    events on the launch stream, rotating over every layer's weights."""
+    """Time the gate/up kernel and the decode step's whole MoE per layer
+    (expert routes, then combine + residual add + next norm, as
+    ``Granite._fused_layers`` runs them) with HIP events, rotating over every
+    layer's weights. Each loop over the 32 layers is recorded into a HIP
+    graph and replayed, so the figures are GPU time, not Python time."""
     import torch
 
     from litemoe_amd import _lib, experts, router
@@ -101,42 +107,56 @@ def moe_roofline(model, cfg, batch, reps):
     H, I, E, k = cfg.hidden_size, cfg.intermediate_size, cfg.num_local_experts, cfg.num_experts_per_tok
     gen = torch.Generator(device=dev).manual_seed(7)
     z = torch.randn(batch, H, device=dev, generator=gen).to(torch.bfloat16)
+    x = torch.randn(batch, H, device=dev, generator=gen).to(torch.bfloat16)
+    z_out = torch.empty_like(z)
     per_layer = []
     for w in model.w["layers"]:
         weights, ids = router.route(z, w["block_sparse_moe.router.layer"], k)
-        offsets, order, _ = experts.moe_align(ids, E)
         act = torch.empty(batch * k, I, device=dev, dtype=torch.bfloat16)
+        y = torch.empty(batch * k, H, device=dev, dtype=torch.bfloat16)
         active = int(torch.unique(ids).numel())
-        per_layer.append((w, weights, ids, offsets, order, act, active))
-    stream = _lib.stream(dev)
-    out = torch.empty(batch, H, device=dev, dtype=torch.bfloat16)
-
+        per_layer.append((w, weights, ids, act, y, active))
     # the weights the decode step reads: the fragment layout when the model packed them
     packed = "input_linear_packed" in model.w["layers"][0]
     w13_key, w2_key = ("input_linear_packed", "output_linear_packed") if packed else ("input_linear",
                                                                                       "output_linear")
+    backend = model.ep.backend  # its workspace, as the model's fused tail uses it
+    r, eps = cfg.residual_multiplier, cfg.rms_norm_eps
+    x0 = x.clone()
 
     def gate_up_all():  # the decode path: each expert's workgroups collect its routes
-        for w, weights, ids, offsets, order, act, _ in per_layer:
+        stream = _lib.stream(dev)
+        for w, weights, ids, act, y, _ in per_layer:
             _lib.call("lm_moe_gate_up_packed" if packed else "lm_moe_gate_up", z.data_ptr(),
                       w[w13_key].data_ptr(), None, None, ids.data_ptr(), batch * k, k, H, I, E, 0,
                       act.data_ptr(), stream)
 
-    def fused_all():
-        for w, weights, ids, *_ in per_layer:
-            experts.fused_experts(z, w[w13_key], w[w2_key], weights, ids, out=out, packed=packed)
+    def moe_all():
+        for w, weights, ids, act, y, _ in per_layer:
+            experts.moe_routes(z, w[w13_key], w[w2_key], ids, workspace=backend.workspace, y=y, packed=packed)
+            experts.finish_add_rmsnorm(y, ids, weights, x, r, w["post_attention_layernorm"], eps, z_out)
 
     result = {}
-    for name, fn in (("gate_up", gate_up_all), ("fused", fused_all)):
-        fn()
+    for name, fn in (("gate_up", gate_up_all), ("fused", moe_all)):
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()  # workspaces allocated outside the recording
+            side.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph.replay()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(reps):
-            fn()
+            graph.replay()
         end.record()
         torch.cuda.synchronize()
-        result[name] = start.elapsed_time(end) * 1e3 / (reps * len(per_layer))  # us per launch
+        result[name] = start.elapsed_time(end) * 1e3 / (reps * len(per_layer))  # us per launch / layer
+    x.copy_(x0)
     active = sum(p[-1] for p in per_layer) / len(per_layer)
     # Algorithmic bytes (weights of active experts + activations in/out).
     gate_up_bytes = active * 2 * I * H * 2 + batch * H * 2 + batch * k * I * 2
@@ -557,7 +577,7 @@ def main():
                    "capacity": engine.capacity, "parallelism": "single GPU",
                    "timed_contexts": [args.prompt, args.prompt + args.steps - 1],
                    "mean_context": round(args.prompt + (args.steps - 1) / 2, 1)},
-        "roofline": {"bound": "hbm", "kernel": "gate_up_scan_kernel (lm_moe_gate_up)",
+        "roofline": {"bound": "hbm", "kernel": "gate_up_scan_kernel (lm_moe_gate_up_packed)",
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("gate_up_scan_kernel.granite3b_b64_decode.txt") if headline else None,
