@@ -133,8 +133,8 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     for (int h = 0; h < kH; ++h)
 #pragma unroll
       for (int i = 0; i < 4; ++i) mt = fmaxf(mt, st[h][i]);
-    mt = fmaxf(mt, shfl_xor(mt, 16));
-    mt = fmaxf(mt, shfl_xor(mt, 32));
+    mt = fmaxf(mt, xor_lanes<16>(mt));  // the four lane groups hold a query's keys
+    mt = fmaxf(mt, xor_lanes<32>(mt));
     const float mn = fmaxf(m, mt * sl2);
     const float corr = factor(m, mn);
     float rs = 0.f;
@@ -150,8 +150,8 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
       pw[2 * h] = pack_bf16_finite(p[0], p[1]);  // p = exp2(finite or -inf): never NaN
       pw[2 * h + 1] = pack_bf16_finite(p[2], p[3]);
     }
-    rs += shfl_xor(rs, 16);
-    rs += shfl_xor(rs, 32);
+    rs += xor_lanes<16>(rs);
+    rs += xor_lanes<32>(rs);
     l = l * corr + rs;
     m = mn;
 

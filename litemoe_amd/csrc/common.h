@@ -80,6 +80,25 @@ __device__ __forceinline__ float wave_sum(float v) {
          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
 }
 
+// The value of lane (lane ^ M) for M in {8, 16, 32}, with VALU lane moves
+// instead of the LDS crossbar (ds_bpermute): DPP row_ror:8 swaps the two
+// halves of each 16-lane row; gfx950's v_permlane16_swap / v_permlane32_swap
+// exchange rows / wave halves between their two operands, and the lane's
+// own half selects which result holds its partner (checked on the device).
+template <int M>
+__device__ __forceinline__ float xor_lanes(float v) {
+  static_assert(M == 8 || M == 16 || M == 32, "lane distance");
+  if constexpr (M == 8) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(__lane_id() < 32 ? r[1] : r[0]);
+  }
+}
+
 // Sum over aligned groups of 8 lanes with DPP lane moves (no LDS crossbar):
 // quad_perm xor 1, quad_perm xor 2, then row_half_mirror (lane i <- 7-i).
 // Every lane of the group ends with the same, bitwise identical sum.
