@@ -80,6 +80,22 @@ struct QkvIn {
 
 constexpr int kMaxQkvSplits = 8;
 
+// a and b summed over lane rows 0+1 and 2+3 (16-lane rows) with one
+// v_permlane16_swap: the swap leaves rows [a0, b0, a2, b2] and [a1, b1, a3, b3],
+// so the sum holds a's pair sums in rows 0 and 2 and b's in rows 1 and 3.
+__device__ __forceinline__ float sum_lane_rows(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// c and d summed over wave halves with one v_permlane32_swap: the swap leaves
+// rows [c0, c1, d0, d1] and [c2, c3, d2, d3]. Applied to two sum_lane_rows
+// results it yields the four values' totals in rows 0, 1, 2, 3.
+__device__ __forceinline__ float sum_row_pairs(float c, float d) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Neox rotation of one (x1, x2) pair with the reference's three roundings
 // (the arithmetic of rope_kv_kernel).
 __device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s, float &o1,
@@ -100,7 +116,8 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
   __shared__ float sm_m[kWaves][G];
   __shared__ float sm_l[kWaves][G];
   __shared__ float sm_qkv[kFused ? G + 2 : 1][kD];
-  __shared__ u32x4 sm_knew[kFused ? kLanesPerKey : 1];  // rotated new key, bf16 words per lane group
+  // Rotated q heads and new key as bf16, 16 bytes per lane group (dc).
+  __shared__ u32x4 sm_rot[kFused ? G + 1 : 1][kLanesPerKey];
   const int split = blockIdx.x, h = blockIdx.y;
   // Workgroups are dispatched in z order; with a row order (rows by
   // descending length) the longest rows start first and a ragged batch ends
@@ -161,15 +178,18 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
       vb[u] = *reinterpret_cast<const u32x4 *>(vbase + (int64_t)j * kD);
     }
   };
-  // Loads complete in issue order: the rotation table row goes first, then
+  // Loads complete in issue order: the rotation table entries go first, then
   // the first two KV iterations, so nothing below waits on the KV stream.
+  // Thread t < (G + 1) * 32 rotates pair t % 32 of head slot t / 32 (the G
+  // q heads, then the new key): channels p and p + 32 of the neox halves.
   const bool in_table = kFused && pnew >= 0 && pnew < in.table_len;
-  const int c0 = 8 * (dc % 4);
-  u32x4 cs_c, cs_s;
+  const int rot_pair = threadIdx.x % (kD / 2);
+  const bool rot_thread = threadIdx.x < (G + 1) * (kD / 2);
+  float cs_c = 0.f, cs_s = 0.f;
   if constexpr (kFused) {
     const bf16 *cs = in.cos_sin + (in_table ? pnew : 0) * kD;
-    cs_c = *reinterpret_cast<const u32x4 *>(cs + c0);
-    cs_s = *reinterpret_cast<const u32x4 *>(cs + kD / 2 + c0);
+    cs_c = bf16_to_f32(cs[rot_pair]);
+    cs_s = bf16_to_f32(cs[kD / 2 + rot_pair]);
   }
   u32x4 ka[kU], va[kU], kb2[kU], vb2[kU];
   load(ka, va, 0);
@@ -179,9 +199,6 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
   u32x4 qw[G];
   const float sl2 = scale * 1.4426950408889634f;
   if constexpr (kFused) {
-    float cf[8], sf[8];
-    unpack8(cs_c, cf);
-    unpack8(cs_s, sf);
     if (threadIdx.x < nstage) {
       const int hs = threadIdx.x / (kD / 4), c4 = (threadIdx.x % (kD / 4)) * 4;
       f32x4 acc4 = pv[0];
@@ -192,46 +209,29 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
       for (int i = 0; i < 4; ++i) sm_qkv[hs][c4 + i] = round_bf16(acc4[i]);
     }
     __syncthreads();
-    // Rotate the (x1, x2) halves of head slot hs; lane dc keeps its half.
-    auto rotated = [&](int hs, float *o) {
-      float r1[8], r2[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float x1 = sm_qkv[hs][c0 + i], x2 = sm_qkv[hs][kD / 2 + c0 + i];
-        if (in_table) {
-          rotate_pair(x1, x2, cf[i], sf[i], r1[i], r2[i]);
-        } else {
-          r1[i] = x1;
-          r2[i] = x2;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = dc < 4 ? r1[i] : r2[i];
-    };
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float qf[8];
-      rotated(g, qf);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qw[g][i] = pack_bf16(qf[2 * i], qf[2 * i + 1]);
+    // Each (head slot, pair) is rotated once per workgroup, not once per wave.
+    if (rot_thread) {
+      const int hs = threadIdx.x / (kD / 2);
+      const float x1 = sm_qkv[hs][rot_pair], x2 = sm_qkv[hs][kD / 2 + rot_pair];
+      float o1 = x1, o2 = x2;
+      if (in_table) rotate_pair(x1, x2, cs_c, cs_s, o1, o2);
+      uint16_t *rot = reinterpret_cast<uint16_t *>(sm_rot[hs]);
+      rot[rot_pair] = (uint16_t)f32_to_bf16(o1);
+      rot[kD / 2 + rot_pair] = (uint16_t)f32_to_bf16(o2);
     }
-    // The rotated new key goes to LDS (for the substitution) and, with the
-    // value, to the cache.
-    if (writer && wave == 0 && ks == 0) {
-      float knew[8];
-      rotated(G, knew);
-      const int64_t at = (((int64_t)b * kv_heads + h) * capacity + pnew) * kD + dc * 8;
-      u32x4 ko, vo;
+    __syncthreads();
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ko[i] = pack_bf16(knew[2 * i], knew[2 * i + 1]);
+    for (int g = 0; g < G; ++g) qw[g] = sm_rot[g][dc];
+    // The rotated new key and the value go to the cache.
+    if (writer && wave == 0 && ks == 0) {
+      const int64_t at = (((int64_t)b * kv_heads + h) * capacity + pnew) * kD + dc * 8;
+      u32x4 vo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
         vo[i] = pack_bf16(sm_qkv[G + 1][dc * 8 + 2 * i], sm_qkv[G + 1][dc * 8 + 2 * i + 1]);
-      }
-      sm_knew[dc] = ko;
-      *reinterpret_cast<u32x4 *>(kc + at) = ko;
+      *reinterpret_cast<u32x4 *>(kc + at) = sm_rot[G][dc];
       *reinterpret_cast<u32x4 *>(vc + at) = vo;
     }
-    if (own) __syncthreads();  // uniform across the workgroup
   } else {
 #pragma unroll
     for (int g = 0; g < G; ++g)
@@ -254,7 +254,7 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
       const bool ok = j < k1;
       u32x4 kw = kb[u];
       if constexpr (kFused) {
-        if (own && j == pnew) kw = sm_knew[dc];
+        if (own && j == pnew) kw = sm_rot[G][dc];
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -320,31 +320,52 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
     load(kb2, vb2, it + 3);
   }
 
-  // Merge the 8 key slots of the wave (lanes with equal dc).
+  // Merge the 8 key slots of the wave (lanes with equal dc). Every slot is
+  // rescaled to the wave's maximum once; the slot sums then pair values
+  // across lane rows (v_permlane16_swap / v_permlane32_swap), so one swap
+  // and one add reduce two values, and finish with one DPP add (lanes l and
+  // l ^ 8). The 9G sums (acc g-major, then l) end in ceil(9G / 4) registers:
+  // value 4k + r in row r (lanes 16r .. 16r + 7, channel group dc) of
+  // register k.
+  constexpr int kVals = 9 * G, kRegs = (kVals + 3) / 4;
+  float vals[4 * kRegs];
 #pragma unroll
-  for (int mask = kLanesPerKey; mask < kWave; mask <<= 1) {
+  for (int g = 0; g < G; ++g) {
+    float mx = fmaxf(m[g], xor_lanes<8>(m[g]));
+    mx = fmaxf(mx, xor_lanes<16>(mx));
+    mx = fmaxf(mx, xor_lanes<32>(mx));
+    // m is finite (kEmpty when the slot saw no key), so f is 0 or a real factor.
+    const float f = __builtin_amdgcn_exp2f(m[g] - mx);
+    m[g] = mx;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mo = shfl_xor(m[g], mask);
-      const float lo = shfl_xor(l[g], mask);
-      const float mn = fmaxf(m[g], mo);
-      const float fa = merge_factor(m[g], mn), fb = merge_factor(mo, mn);
-      l[g] = l[g] * fa + lo * fb;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] = acc[g][i] * fa + shfl_xor(acc[g][i], mask) * fb;
-      m[g] = mn;
-    }
+    for (int i = 0; i < 8; ++i) vals[8 * g + i] = acc[g][i] * f;
+    vals[8 * G + g] = l[g] * f;
   }
-  if (ks == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+  for (int v = kVals; v < 4 * kRegs; ++v) vals[v] = 0.f;
+  float sums[kRegs];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sm_o[wave][g][dc * 8 + i] = acc[g][i];
-      if (dc == 0) {
-        sm_m[wave][g] = m[g];
-        sm_l[wave][g] = l[g];
+  for (int k = 0; k < kRegs; ++k) {
+    const float t = sum_row_pairs(sum_lane_rows(vals[4 * k], vals[4 * k + 1]),
+                                  sum_lane_rows(vals[4 * k + 2], vals[4 * k + 3]));
+    sums[k] = t + xor_lanes<8>(t);
+  }
+  if ((lane & 8) == 0) {  // ks even: one lane per (row, dc)
+    const int r = lane / 16;
+#pragma unroll
+    for (int k = 0; k < kRegs; ++k) {
+      if (k < 2 * G) {
+        sm_o[wave][k / 2][dc * 8 + 4 * (k % 2) + r] = sums[k];
+      } else {
+        const int gl = 4 * (k - 2 * G) + r;
+        if (dc == 0 && gl < G) sm_l[wave][gl] = sums[k];
       }
     }
+  }
+  if (lane < G) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (lane == g) sm_m[wave][g] = m[g];
   }
   __syncthreads();
   // Threads (g, channel) merge the waves.
