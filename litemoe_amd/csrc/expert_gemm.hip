@@ -5,7 +5,12 @@
 //
 // over the route blocks of lm_moe_align (routes sorted by expert; a block is
 // at most 128 routes of one expert, found on the device from the offsets).
-// act and y are in route order r = t*topk + branch, as on the decode path.
+// y is in route order r = t*topk + branch, as on the decode path; act is in
+// route order for the public gate_up / down entry points and in sorted order
+// (row = position in the expert-sorted route list) between the two GEMMs of
+// one fused call, so that down reads each route block's act rows as one
+// contiguous run instead of gathering 128-byte pieces of rows spread over
+// the whole buffer.
 //
 // Workgroup = (output column tile, route block), 4 waves. It computes a
 // kTM x kTN fp32 tile (128 x 128 by default): for gate_up the B tile is
@@ -26,6 +31,7 @@
 // Reference: the expert math of litemoe/ops.py:43-47 (reference_experts) and
 // vLLM fused_experts at litemoe/ep.py:40-41.
 #include <algorithm>
+#include <type_traits>
 
 #include "internal.h"
 
@@ -84,7 +90,8 @@ __device__ __forceinline__ int frag_offset(int row, int chunk) {
 // kPacked: weights in the fragment layout of lm_expert_pack (a load
 // instruction then reads eight whole 128-byte runs: the 8 rows of one
 // (k-step, k-group) are adjacent there).
-template <bool kGateUp, int kTM, int kTN, int kStages, bool kPacked>
+// kSortedAct: act row of sorted position p is p (gate_up writes, down reads).
+template <bool kGateUp, int kTM, int kTN, int kStages, bool kPacked, bool kSortedAct>
 __global__ void __launch_bounds__(kThreads, kTM * kTN > 128 * 128 ? 1 : 4 - kStages)
 expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
                    const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
@@ -119,8 +126,13 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   int oa[kLA], ob[kLB];  // element offsets (< 2^31 at the supported sizes)
 #pragma unroll
   for (int i = 0; i < kLA; ++i) {
-    const int route = route_of[8 * (wave * kLA + i) + lane / 8];
-    oa[i] = (kGateUp ? route / topk : route) * K + chunk * 8;
+    const int t = 8 * (wave * kLA + i) + lane / 8;
+    if constexpr (!kGateUp && kSortedAct) {
+      oa[i] = (r0 + min(t, n - 1)) * K + chunk * 8;
+    } else {
+      const int route = route_of[t];
+      oa[i] = (kGateUp ? route / topk : route) * K + chunk * 8;
+    }
   }
 #pragma unroll
   for (int i = 0; i < kLB; ++i) {
@@ -211,7 +223,8 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
     for (int i = 0; i < 4; ++i) {
       const int row = wr * (kTM / 2) + rb * 16 + 4 * fk + i;
       if (row >= n) continue;
-      bf16 *o = out + (int64_t)route_of[row] * out_cols + c0;
+      const int64_t orow = kGateUp && kSortedAct ? r0 + row : route_of[row];
+      bf16 *o = out + orow * out_cols + c0;
       if constexpr (kGateUp) {
 #pragma unroll
         for (int cb = 0; cb < kCB / 2; ++cb) {
@@ -239,32 +252,45 @@ bool expert_gemm_ok(int64_t routes, int64_t hidden, int64_t inter, int64_t exper
 int launch_expert_gemm_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets,
                                const int32_t *sorted, int64_t routes, int64_t topk, int64_t hidden,
                                int64_t inter, int64_t experts, bf16 *act, bool packed,
-                               hipStream_t stream) {
+                               bool sorted_act, hipStream_t stream) {
   const int64_t blocks = align_up(cdiv(routes, kTile) + experts, kXcds);
   if (blocks > 65535) return LM_EUNSUPPORTED;
   const dim3 grid((unsigned)(2 * inter / kTile), (unsigned)blocks);
-  if (packed)
-    expert_gemm_kernel<true, kTile, kTile, kLdsStages, true><<<grid, kThreads, 0, stream>>>(
+  auto go = [&](auto packed_c, auto sorted_c) {
+    expert_gemm_kernel<true, kTile, kTile, kLdsStages, decltype(packed_c)::value,
+                       decltype(sorted_c)::value><<<grid, kThreads, 0, stream>>>(
         x, w13, offsets, sorted, (int)topk, (int)hidden, (int)inter, (int)inter, (int)experts, act);
-  else
-    expert_gemm_kernel<true, kTile, kTile, kLdsStages, false><<<grid, kThreads, 0, stream>>>(
-        x, w13, offsets, sorted, (int)topk, (int)hidden, (int)inter, (int)inter, (int)experts, act);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  if (packed) {
+    if (sorted_act) go(T{}, T{}); else go(T{}, F{});
+  } else {
+    if (sorted_act) go(F{}, T{}); else go(F{}, F{});
+  }
   LM_CHECK_LAUNCH();
   return LM_OK;
 }
 
 int launch_expert_gemm_down(const bf16 *act, const bf16 *w2, const int32_t *offsets,
                             const int32_t *sorted, int64_t routes, int64_t hidden, int64_t inter,
-                            int64_t experts, bf16 *y, bool packed, hipStream_t stream) {
+                            int64_t experts, bf16 *y, bool packed, bool sorted_act,
+                            hipStream_t stream) {
   const int64_t blocks = align_up(cdiv(routes, kTile) + experts, kXcds);
   if (blocks > 65535) return LM_EUNSUPPORTED;
   const dim3 grid((unsigned)(hidden / kTile), (unsigned)blocks);
-  if (packed)
-    expert_gemm_kernel<false, kTile, kTile, kLdsStages, true><<<grid, kThreads, 0, stream>>>(
+  auto go = [&](auto packed_c, auto sorted_c) {
+    expert_gemm_kernel<false, kTile, kTile, kLdsStages, decltype(packed_c)::value,
+                       decltype(sorted_c)::value><<<grid, kThreads, 0, stream>>>(
         act, w2, offsets, sorted, 1, (int)inter, (int)hidden, (int)inter, (int)experts, y);
-  else
-    expert_gemm_kernel<false, kTile, kTile, kLdsStages, false><<<grid, kThreads, 0, stream>>>(
-        act, w2, offsets, sorted, 1, (int)inter, (int)hidden, (int)inter, (int)experts, y);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  if (packed) {
+    if (sorted_act) go(T{}, T{}); else go(T{}, F{});
+  } else {
+    if (sorted_act) go(F{}, T{}); else go(F{}, F{});
+  }
   LM_CHECK_LAUNCH();
   return LM_OK;
 }

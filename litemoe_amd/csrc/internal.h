@@ -62,9 +62,12 @@ bool expert_gemm_ok(int64_t routes, int64_t hidden, int64_t inter, int64_t exper
 int launch_expert_gemm_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets,
                                const int32_t *sorted, int64_t routes, int64_t topk, int64_t hidden,
                                int64_t inter, int64_t experts, bf16 *act, bool packed,
-                               hipStream_t stream);
+                               bool sorted_act, hipStream_t stream);
+// sorted_act: act rows in expert-sorted route order (gate_up writes row p for
+// sorted position p, down reads it there) instead of route order.
 int launch_expert_gemm_down(const bf16 *act, const bf16 *w2, const int32_t *offsets,
                             const int32_t *sorted, int64_t routes, int64_t hidden, int64_t inter,
-                            int64_t experts, bf16 *y, bool packed, hipStream_t stream);
+                            int64_t experts, bf16 *y, bool packed, bool sorted_act,
+                            hipStream_t stream);
 
 }  // namespace lm

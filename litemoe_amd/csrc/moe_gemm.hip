@@ -623,7 +623,8 @@ ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, 
   return w;
 }
 
-// act and y in route order.
+// y in route order; act in route order on the scan and block paths, in
+// sorted order between the two expert GEMMs.
 int run_routes(const void *x, const void *w13, const void *w2, const int32_t *topk_ids,
                int64_t tokens, int64_t hidden, int64_t inter, int64_t experts, int64_t topk,
                int64_t block_rows, bf16 *y, const ExpertWorkspace &w, bool packed, void *stream) {
@@ -641,11 +642,12 @@ int run_routes(const void *x, const void *w13, const void *w2, const int32_t *to
                         w.align_scratch, w.align_bytes, s);
   if (rc) return rc;
   if (block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts)) {
+    // act stays internal here: sorted order, read contiguously by down.
     rc = launch_expert_gemm_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, routes,
-                                    topk, hidden, inter, experts, w.act, packed, s);
+                                    topk, hidden, inter, experts, w.act, packed, true, s);
     if (rc) return rc;
     return launch_expert_gemm_down(w.act, (const bf16 *)w2, w.offsets, w.sorted, routes, hidden,
-                                   inter, experts, y, packed, s);
+                                   inter, experts, y, packed, true, s);
   }
   rc = launch_gate_up((const bf16 *)x, (const bf16 *)w13, w.offsets, w.sorted, nullptr, routes,
                       topk, hidden, inter, experts, bm, w.act, packed, s);
@@ -682,7 +684,7 @@ int moe_gate_up(const void *x, const void *w13, const int32_t *expert_offsets,
   if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts))
     return launch_expert_gemm_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets,
                                       sorted_routes, routes, topk, hidden, inter, experts,
-                                      (bf16 *)act, packed, (hipStream_t)stream);
+                                      (bf16 *)act, packed, false, (hipStream_t)stream);
   return launch_gate_up((const bf16 *)x, (const bf16 *)w13, expert_offsets, sorted_routes, topk_ids,
                         routes, topk, hidden, inter, experts, pick_block_rows(block_rows, routes),
                         (bf16 *)act, packed, (hipStream_t)stream);
@@ -700,7 +702,7 @@ int moe_down(const void *act, const void *w2, const int32_t *expert_offsets,
   if (!topk_ids && block_rows == 0 && expert_gemm_ok(routes, hidden, inter, experts))
     return launch_expert_gemm_down((const bf16 *)act, (const bf16 *)w2, expert_offsets,
                                    sorted_routes, routes, hidden, inter, experts, (bf16 *)y, packed,
-                                   (hipStream_t)stream);
+                                   false, (hipStream_t)stream);
   return launch_down((const bf16 *)act, (const bf16 *)w2, expert_offsets, sorted_routes, topk_ids,
                      routes, hidden, inter, experts, pick_block_rows(block_rows, routes), (bf16 *)y,
                      packed, (hipStream_t)stream);
