@@ -411,7 +411,10 @@ def test_finish_never_reads_all_nonlocal_nan_rows():
 
 @pytest.mark.parametrize("b,hq,hkv,cap,low,high,splits", [
     (64, 24, 8, 2048, 1, 1280, None), (32, 16, 8, 1024, 1, 640, 1), (5, 24, 8, 256, 1, 256, 3),
-    (128, 24, 8, 4096, 1024, 4096, None)])
+    (128, 24, 8, 4096, 1024, 4096, None),
+    # the other query-group sizes the kernel is built for (q heads per kv head 1, 4, 6, 8)
+    (4, 8, 8, 256, 1, 256, None), (6, 32, 8, 512, 1, 512, None), (3, 48, 8, 300, 1, 300, 2),
+    (5, 64, 8, 512, 1, 512, None)])
 @torch.inference_mode()
 def test_flash_decode_matches_oracle(b, hq, hkv, cap, low, high, splits):
     g = torch.Generator().manual_seed(b + cap)

@@ -79,7 +79,7 @@ def _qkv_case(b, hq, hkv, cap, splits, seed):
 
 @pytest.mark.parametrize("b,hq,hkv,cap,attn_splits,qkv_splits", [
     (64, 24, 8, 1280, 1, 3), (5, 24, 8, 1024, 4, 3), (3, 16, 8, 300, 3, 2), (7, 8, 8, 64, 1, 8),
-    (2, 32, 4, 2048, 16, 1)])
+    (2, 32, 4, 2048, 16, 1), (9, 24, 6, 512, 2, 3), (4, 24, 4, 700, 1, 2)])
 @torch.inference_mode()
 def test_flash_decode_qkv_equals_unfused(b, hq, hkv, cap, attn_splits, qkv_splits):
     part, cos_sin, pos = _qkv_case(b, hq, hkv, cap, qkv_splits, b * cap)
