@@ -1,8 +1,9 @@
 // Packed variable-length (causal) attention on MFMA, head_dim 64.
 //
-// Workgroup (query block of 64, q head, sequence); wave w owns 16 queries.
-// Keys stream in tiles of 32 staged through LDS, K and V both row-major; the
-// next tile is loaded into registers while the current one is computed.
+// Workgroup (query block of 128, q head, sequence); wave w owns two 16-query
+// sub-blocks. Keys stream in tiles of 64 staged through LDS, K and V both
+// row-major; the next tile is loaded into registers while the current one is
+// computed.
 // Scores are computed transposed, S^T = K . Q^T, so each lane's C fragment
 // (keys 16h + 4*(l/16) + i, query l%16) is directly the A operand of P . V:
 // the eight keys a lane holds become the eight k slots of one
@@ -22,7 +23,6 @@ namespace {
 
 constexpr int kD = 64;
 constexpr int kThreads = 256;
-constexpr int kBQ = 64;
 constexpr int kBK = 64;
 constexpr int kStage = kBK / 32;  // keys each staging thread loads per tile (one per 32)
 constexpr int kKPad = 8;
@@ -43,11 +43,18 @@ __device__ __forceinline__ uint2 read_tr(const bf16 *p) {
                (uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16)};
 }
 
+// kQS 16-query sub-blocks per wave (kBQ = 64 * kQS queries per workgroup):
+// every K fragment and transposed V read feeds kQS MFMAs, and the sub-blocks'
+// softmax chains are independent, so a wave has kQS chains to interleave.
+// Per query the arithmetic is the same for every kQS (a tile that is fully
+// masked for one sub-block adds exact zeros to its state).
+template <int kQS>
 __global__ void __launch_bounds__(kThreads)
 prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 *__restrict__ k,
                int64_t ks0, int64_t ks1, const bf16 *__restrict__ v, int64_t vs0, int64_t vs1,
                const int32_t *__restrict__ cu, int q_heads, int kv_heads, float scale, int causal,
                bf16 *__restrict__ out) {
+  constexpr int kBQ = 64 * kQS;
   __shared__ __attribute__((aligned(16))) bf16 ks_lds[kBK][kD + kKPad];
   __shared__ __attribute__((aligned(16))) bf16 vs_lds[kBK][kD + kKPad];
   const int qb = blockIdx.x, hq = blockIdx.y, seq = blockIdx.z;
@@ -58,20 +65,28 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
   const int hk = hq / (q_heads / kv_heads);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
-  const int wq0 = q0 + wave * 16;
-  const int qi = wq0 + col;  // this lane's query (softmax state owner)
+  const int wq0 = q0 + wave * 16 * kQS;  // the wave's first query
   const float sl2 = scale * 1.4426950408889634f;
 
-  u32x4 qf0 = {0u, 0u, 0u, 0u}, qf1 = {0u, 0u, 0u, 0u};
-  if (qi < len) {
-    const bf16 *qp = q + (int64_t)(start + qi) * qs0 + (int64_t)hq * qs1 + grp * 8;
-    qf0 = *reinterpret_cast<const u32x4 *>(qp);
-    qf1 = *reinterpret_cast<const u32x4 *>(qp + 32);
-  }
-  float m = -INFINITY, l = 0.f;
-  f32x4 o[4];
+  // Sub-block qs: queries wq0 + 16 qs + (0..15); lane col owns query
+  // wq0 + 16 qs + col's softmax state.
+  u32x4 qf0[kQS], qf1[kQS];
+  float m[kQS], l[kQS];
+  f32x4 o[kQS][4];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int qs = 0; qs < kQS; ++qs) {
+    const int qi = wq0 + 16 * qs + col;
+    qf0[qs] = qf1[qs] = u32x4{0u, 0u, 0u, 0u};
+    if (qi < len) {
+      const bf16 *qp = q + (int64_t)(start + qi) * qs0 + (int64_t)hq * qs1 + grp * 8;
+      qf0[qs] = *reinterpret_cast<const u32x4 *>(qp);
+      qf1[qs] = *reinterpret_cast<const u32x4 *>(qp + 32);
+    }
+    m[qs] = -INFINITY;
+    l[qs] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[qs][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   const int kend = causal ? min(len, q0 + kBQ) : len;
   const bool wave_live = wq0 < len;
@@ -104,94 +119,108 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     __syncthreads();
     // The next tile streams in while this one is computed.
     load(min(kt + kBK, kend - 1), kv, vv);
-    if (!wave_live || (causal && kt > wq0 + 15)) continue;
+    if (!wave_live || (causal && kt > wq0 + 16 * kQS - 1)) continue;
     constexpr int kH = kBK / 16;  // 16-key blocks of the tile
-    f32x4 st[kH];
+    f32x4 st[kQS][kH];
 #pragma unroll
     for (int h = 0; h < kH; ++h) {
       const u32x4 a0 = *reinterpret_cast<const u32x4 *>(&ks_lds[16 * h + col][grp * 8]);
       const u32x4 a1 = *reinterpret_cast<const u32x4 *>(&ks_lds[16 * h + col][32 + grp * 8]);
-      st[h] = mfma16x16x32(a0, qf0, f32x4{0.f, 0.f, 0.f, 0.f});
-      st[h] = mfma16x16x32(a1, qf1, st[h]);
+#pragma unroll
+      for (int qs = 0; qs < kQS; ++qs) {
+        st[qs][h] = mfma16x16x32(a0, qf0[qs], f32x4{0.f, 0.f, 0.f, 0.f});
+        st[qs][h] = mfma16x16x32(a1, qf1[qs], st[qs][h]);
+      }
     }
     // Only a tile past the sequence end or crossing the causal diagonal of
     // this wave's queries has masked scores.
     const bool masking = kt + kBK > len || (causal && kt + kBK - 1 > wq0);
     if (masking) {
 #pragma unroll
+      for (int qs = 0; qs < kQS; ++qs)
+#pragma unroll
+        for (int h = 0; h < kH; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = kt + 16 * h + grp * 4 + i;
+            if (j >= len || (causal && j > wq0 + 16 * qs + col)) st[qs][h][i] = -INFINITY;
+          }
+    }
+    uint32_t pw[kQS][2 * kH];
+#pragma unroll
+    for (int qs = 0; qs < kQS; ++qs) {
+      // The maximum is taken on the raw dot products (the scale is
+      // positive), and exp2(s * scale*log2e - m) is one FMA and one v_exp_f32.
+      float mt = -INFINITY;
+#pragma unroll
       for (int h = 0; h < kH; ++h)
 #pragma unroll
+        for (int i = 0; i < 4; ++i) mt = fmaxf(mt, st[qs][h][i]);
+      mt = fmaxf(mt, xor_lanes<16>(mt));  // the four lane groups hold a query's keys
+      mt = fmaxf(mt, xor_lanes<32>(mt));
+      const float mn = fmaxf(m[qs], mt * sl2);
+      const float corr = factor(m[qs], mn);
+      float rs = 0.f;
+#pragma unroll
+      for (int h = 0; h < kH; ++h) {
+        float p[4];
+#pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int j = kt + 16 * h + grp * 4 + i;
-          if (j >= len || (causal && j > qi)) st[h][i] = -INFINITY;
+          p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qs][h][i], sl2, -mn));  // exp2(-inf) = 0; mn is finite
+          rs += p[i];
         }
-    }
-    // The maximum is taken on the raw dot products (the scale is positive),
-    // and exp2(s * scale*log2e - m) is one FMA and one v_exp_f32.
-    float mt = -INFINITY;
-#pragma unroll
-    for (int h = 0; h < kH; ++h)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mt = fmaxf(mt, st[h][i]);
-    mt = fmaxf(mt, xor_lanes<16>(mt));  // the four lane groups hold a query's keys
-    mt = fmaxf(mt, xor_lanes<32>(mt));
-    const float mn = fmaxf(m, mt * sl2);
-    const float corr = factor(m, mn);
-    float rs = 0.f;
-    uint32_t pw[2 * kH];
-#pragma unroll
-    for (int h = 0; h < kH; ++h) {
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[h][i], sl2, -mn));  // exp2(-inf) = 0; mn is finite
-        rs += p[i];
+        pw[qs][2 * h] = pack_bf16_finite(p[0], p[1]);  // p = exp2(finite or -inf): never NaN
+        pw[qs][2 * h + 1] = pack_bf16_finite(p[2], p[3]);
       }
-      pw[2 * h] = pack_bf16_finite(p[0], p[1]);  // p = exp2(finite or -inf): never NaN
-      pw[2 * h + 1] = pack_bf16_finite(p[2], p[3]);
-    }
-    rs += xor_lanes<16>(rs);
-    rs += xor_lanes<32>(rs);
-    l = l * corr + rs;
-    m = mn;
+      rs += xor_lanes<16>(rs);
+      rs += xor_lanes<32>(rs);
+      l[qs] = l[qs] * corr + rs;
+      m[qs] = mn;
 
-    // O rows held by this lane are queries 4*grp + i of the wave; the
-    // rescale is skipped when no query of the wave moved its maximum.
-    if (__ballot(corr != 1.f)) {
-      float rc[4];
+      // O rows held by this lane are queries 4*grp + i of the sub-block; the
+      // rescale is skipped when no query of the sub-block moved its maximum.
+      if (__ballot(corr != 1.f)) {
+        float rc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rc[i] = __shfl(corr, grp * 4 + i, kWave);
+        for (int i = 0; i < 4; ++i) rc[i] = __shfl(corr, grp * 4 + i, kWave);
 #pragma unroll
-      for (int d = 0; d < 4; ++d)
+        for (int d = 0; d < 4; ++d)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[d][i] *= rc[i];
+          for (int i = 0; i < 4; ++i) o[qs][d][i] *= rc[i];
+      }
     }
     // Each 32 keys of the tile are one P.V step: keys 32c + (the two
     // 16-key blocks' rows) as the eight k slots.
 #pragma unroll
     for (int c = 0; c < kBK / 32; ++c) {
-      const u32x4 pa = {pw[4 * c], pw[4 * c + 1], pw[4 * c + 2], pw[4 * c + 3]};
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const uint2 lo = read_tr(&vs_lds[32 * c + trow][d * 16 + tch]);
         const uint2 hi = read_tr(&vs_lds[32 * c + 16 + trow][d * 16 + tch]);
         const u32x4 vb = {lo.x, lo.y, hi.x, hi.y};
-        o[d] = mfma16x16x32(pa, vb, o[d]);
+#pragma unroll
+        for (int qs = 0; qs < kQS; ++qs) {
+          const u32x4 pa = {pw[qs][4 * c], pw[qs][4 * c + 1], pw[qs][4 * c + 2], pw[qs][4 * c + 3]};
+          o[qs][d] = mfma16x16x32(pa, vb, o[qs][d]);
+        }
       }
     }
   }
   if (!wave_live) return;
-  float rl[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) rl[i] = __shfl(l, grp * 4 + i, kWave);
+  for (int qs = 0; qs < kQS; ++qs) {
+    float rl[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int qq = wq0 + grp * 4 + i;
-    if (qq >= len) continue;
-    bf16 *op = out + ((int64_t)(start + qq) * q_heads + hq) * kD;
+    for (int i = 0; i < 4; ++i) rl[i] = __shfl(l[qs], grp * 4 + i, kWave);
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-      op[d * 16 + col] = (bf16)f32_to_bf16(rl[i] > 0.f ? o[d][i] / rl[i] : 0.f);
+    for (int i = 0; i < 4; ++i) {
+      const int qq = wq0 + 16 * qs + grp * 4 + i;
+      if (qq >= len) continue;
+      bf16 *op = out + ((int64_t)(start + qq) * q_heads + hq) * kD;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        op[d * 16 + col] = (bf16)f32_to_bf16(rl[i] > 0.f ? o[qs][d][i] / rl[i] : 0.f);
+    }
   }
 }
 
@@ -211,8 +240,15 @@ extern "C" int lm_prefill_attention(const void *q, int64_t qs0, int64_t qs1, con
   if (head_dim != kD) return LM_EUNSUPPORTED;
   if (num_seqs == 0 || tokens == 0 || max_len == 0) return LM_OK;
   LM_REQUIRE(q && k && v && cu_seqlens && out);
-  const dim3 grid((unsigned)cdiv(max_len, kBQ), (unsigned)q_heads, (unsigned)num_seqs);
-  prefill_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(
+// Two sub-blocks per wave: 0.46 -> 0.41 ms per layer at cfg 4 with the
+// accumulators in VGPRs (built that way); in the AGPR form the second
+// sub-block costs occupancy and is slower than one.
+#ifndef LM_PREFILL_QSUB
+#define LM_PREFILL_QSUB 2
+#endif
+  constexpr int kQS = LM_PREFILL_QSUB;
+  const dim3 grid((unsigned)cdiv(max_len, 64 * kQS), (unsigned)q_heads, (unsigned)num_seqs);
+  prefill_kernel<kQS><<<grid, kThreads, 0, (hipStream_t)stream>>>(
       (const bf16 *)q, qs0, qs1, (const bf16 *)k, ks0, ks1, (const bf16 *)v, vs0, vs1, cu_seqlens,
       (int)q_heads, (int)kv_heads, scale, causal, (bf16 *)out);
   LM_CHECK_LAUNCH();
