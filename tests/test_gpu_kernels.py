@@ -475,6 +475,26 @@ def test_prefill_attention_matches_oracle_and_isolates_sequences(lengths):
     assert not torch.equal(changed[1:end], got[1:end])
 
 
+@pytest.mark.parametrize("lengths,hq,hkv,causal", [
+    ([1, 17, 64, 65, 130, 300], 24, 8, False),   # non-causal: every key of the sequence
+    ([3, 0, 129, 5], 16, 8, True),               # an empty sequence inside the pack
+    ([250, 1, 128], 8, 8, True),                 # one q head per kv head
+    ([257, 31], 32, 4, False)])
+@torch.inference_mode()
+def test_prefill_attention_modes_and_head_ratios(lengths, hq, hkv, causal):
+    t = sum(lengths)
+    g = torch.Generator().manual_seed(t + hq)
+    q = torch.randn(t, hq, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(t, hkv, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(t, hkv, 64, generator=g).to(torch.bfloat16)
+    cu = torch.tensor([0] + lengths).cumsum(0).to(torch.int32)
+    got = packed.varlen_attention(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), max(lengths), 0.125,
+                                  causal=causal).cpu()
+    exp = ops.varlen_attention(q, k, v, cu, 0.125, causal=causal)
+    torch.testing.assert_close(got, exp, atol=.016, rtol=.016)
+    assert rel_l2(got, exp) < 1e-2
+
+
 # ----------------------------------------------------------- fused decode ops --
 
 @pytest.mark.parametrize("m", [1, 16, 64, 256, 257])
