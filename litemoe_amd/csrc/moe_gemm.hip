@@ -119,6 +119,25 @@ __device__ int scan_ids(const ScanIds &s, int e, int *list, int *wave_count) {
   return total;
 }
 
+constexpr int kXcdCount = 8;
+
+// Expert e's column tiles all on XCD e % 8 (workgroups are dealt to the 8
+// XCDs round-robin in dispatch order), so its activation rows are fetched
+// into one L2 and the down kernel finds the act rows in the L2 that wrote
+// them. Identity when the expert count is not a multiple of 8.
+__device__ __forceinline__ void xcd_tile(int &e, int &tile) {
+  const int tiles = gridDim.x, experts = gridDim.y;
+  if (experts % kXcdCount) {
+    e = blockIdx.y;
+    tile = blockIdx.x;
+    return;
+  }
+  const int lin = blockIdx.y * tiles + blockIdx.x;
+  const int j = lin / kXcdCount;
+  e = lin % kXcdCount + kXcdCount * (j / tiles);
+  tile = j % tiles;
+}
+
 __device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
 struct RouteSet {
@@ -234,7 +253,9 @@ gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
   __shared__ int wave_count[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
-  const int e = blockIdx.y, n0 = blockIdx.x * 16;
+  int e, tile;
+  xcd_tile(e, tile);
+  const int n0 = tile * 16;
   const int kbase = wave * KS * 32 + grp * 8;
   const int64_t rg = (int64_t)e * 2 * inter + n0 + col;
   const bf16 *wg = w13 + wofs<kPacked>(rg, kbase, hidden);
@@ -393,7 +414,9 @@ down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
   __shared__ int wave_count[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
-  const int e = blockIdx.y, n0 = blockIdx.x * 16 * NT;
+  int e, tile;
+  xcd_tile(e, tile);
+  const int n0 = tile * 16 * NT;
   const int kbase = wave * KS * 32 + grp * 8;
   const int64_t r0 = (int64_t)e * hidden + n0 + col;
   u32x4 b[NT][KS], a[KS];
