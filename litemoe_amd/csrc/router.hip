@@ -499,26 +499,32 @@ void launch_fast_router(int nv, int64_t tokens, bf16 *x, const bf16 *a, float al
   }
 }
 
-// Prefill-sized router: a workgroup of four waves routes kBatchRows = 16
+// Prefill-sized router: a workgroup of four waves routes kBatchRows = 32
 // tokens, for experts <= 64 and hidden = 512 * NVL.
-//  1. (kNorm) Wave w normalises tokens 4w..4w+3 in turn, with the next
+//  1. (kNorm) Wave w normalises tokens 8w..8w+7 in turn, with the next
 //     token's loads in flight: lane l holds 16-byte words l + 64i (i < NVL),
 //     the words threads l + 64j of rmsnorm_kernel hold (word (l + 64j) +
 //     256v for i = j + 4v). The sum of squares is kept per j in that
 //     thread's order and reduced by wave_sum per j, then over j in order, so
 //     x and z are bitwise the unfused kernels'.
-//  2. The 16 rows of z (x when !kNorm) are read back as MFMA A operands and
-//     the gate rows as B operands (both from L2); wave w accumulates k-steps
-//     [w K/4, (w+1) K/4) of the 16 x 16*NT logits with
+//  2. The 32 rows of z (x when !kNorm) are read back as MFMA A operands, two
+//     16-row blocks, and the gate rows as B operands (both from L2), each
+//     gate fragment feeding both blocks; wave w accumulates k-steps
+//     [w K/4, (w+1) K/4) of the 32 x 16*NT logits with
 //     v_mfma_f32_16x16x32_bf16, and the four partial tiles are summed in
-//     wave order through LDS and rounded to bf16 (and to logits_out).
-//  3. Wave w selects the top-k of tokens 4w..4w+3 (select_topk_lanes).
+//     wave order through LDS and rounded to bf16 (and to logits_out). Per
+//     row the accumulation order is that of a 16-row workgroup; 32 rows halve
+//     the gate-weight reads (147 KB from L2 per workgroup at the 3B shape):
+//     178 -> 155 us per call at 46,990 tokens; 64 rows (two workgroups per
+//     CU) 171 us.
+//  3. Wave w selects the top-k of tokens 8w..8w+7 (select_topk_lanes).
 // The logits accumulate in the matrix core's order rather than
 // router_gemv's, so a logit can differ from the GEMV kernels' by one bf16
 // ulp (as a BLAS GEMM's order can); the selection is exact given the
-// logits. All 16 rows must exist (the caller routes a tail of fewer tokens
+// logits. All 32 rows must exist (the caller routes a tail of fewer tokens
 // with the per-token kernels).
-constexpr int kBatchRows = 16;
+constexpr int kBatchMB = 2;  // 16-row MFMA blocks per workgroup: each gate fragment feeds kBatchMB
+constexpr int kBatchRows = 16 * kBatchMB;
 constexpr int kBatchWaves = 4;
 constexpr int kBatchThreads = kBatchWaves * kWave;
 constexpr int kRowsPerWave = kBatchRows / kBatchWaves;
@@ -526,7 +532,7 @@ constexpr int kRowsPerWave = kBatchRows / kBatchWaves;
 #define LM_BATCH_ROUTER_MIN_TOKENS 1024
 #endif
 constexpr int64_t kBatchRouterMinTokens = LM_BATCH_ROUTER_MIN_TOKENS;
-constexpr int kBatchSteps = 4;  // k-steps whose operand loads are issued together
+constexpr int kBatchSteps = 4 / kBatchMB;  // k-steps whose operand loads are issued together
 
 template <int NVL, bool kAdd>
 __device__ __forceinline__ void batch_load_row(const bf16 *__restrict__ x,
@@ -598,7 +604,7 @@ batched_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float al
   constexpr int kNvec = NVL * kWave, kSteps = NVL * 16, kCols = NT * 16;
   constexpr int kWaveSteps = kSteps / kBatchWaves;
   static_assert(kWaveSteps % kBatchSteps == 0, "k-steps per load batch");
-  __shared__ __align__(16) float part[kBatchWaves][NT][4][kWave];
+  __shared__ __align__(16) float part[kBatchWaves][kBatchMB][NT][4][kWave];
   __shared__ __align__(16) float logit[kBatchRows][kCols];
   __shared__ __align__(16) float scratch[kBatchWaves][2 * kWave];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -622,38 +628,47 @@ batched_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float al
   const int tr = lane % 16, kg = lane / 16;
   const int64_t k0 = (int64_t)wave * kWaveSteps * 4 + kg;  // 16-byte word of the wave's first k-step
   const u32x4 *ap = reinterpret_cast<const u32x4 *>(kNorm ? z : x) + (row0 + tr) * kNvec + k0;
+  constexpr int64_t kBlockStride = 16 * (int64_t)kNvec;  // the next 16-row block of A
   const u32x4 *bp[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
     bp[n] = reinterpret_cast<const u32x4 *>(wr) + (int64_t)min(16 * n + tr, experts - 1) * kNvec + k0;
-  f32x4 acc[NT];
+  f32x4 acc[kBatchMB][NT];
 #pragma unroll
-  for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mb = 0; mb < kBatchMB; ++mb)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[mb][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < kWaveSteps; s0 += kBatchSteps) {
-    u32x4 av[kBatchSteps], bv[kBatchSteps][NT];
+    u32x4 av[kBatchSteps][kBatchMB], bv[kBatchSteps][NT];
 #pragma unroll
     for (int u = 0; u < kBatchSteps; ++u) {
-      av[u] = ap[4 * (s0 + u)];
+#pragma unroll
+      for (int mb = 0; mb < kBatchMB; ++mb) av[u][mb] = ap[mb * kBlockStride + 4 * (s0 + u)];
 #pragma unroll
       for (int n = 0; n < NT; ++n) bv[u][n] = bp[n][4 * (s0 + u)];
     }
 #pragma unroll
     for (int u = 0; u < kBatchSteps; ++u)
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[n] = mfma16x16x32(av[u], bv[u][n], acc[n]);
+      for (int mb = 0; mb < kBatchMB; ++mb)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[mb][n] = mfma16x16x32(av[u][mb], bv[u][n], acc[mb][n]);
   }
 #pragma unroll
-  for (int n = 0; n < NT; ++n)
+  for (int mb = 0; mb < kBatchMB; ++mb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) part[wave][n][i][lane] = acc[n][i];
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[wave][mb][n][i][lane] = acc[mb][n][i];
   __syncthreads();
   // C layout: lane l of a tile holds rows 4*(l/16) + i of column l % 16.
-  for (int idx = threadIdx.x; idx < NT * 4 * kWave; idx += kBatchThreads) {
-    const int n = idx / (4 * kWave), i = idx / kWave % 4, l = idx % kWave;
-    float sum = part[0][n][i][l];
+  for (int idx = threadIdx.x; idx < kBatchMB * NT * 4 * kWave; idx += kBatchThreads) {
+    const int mb = idx / (NT * 4 * kWave), n = idx / (4 * kWave) % NT, i = idx / kWave % 4,
+              l = idx % kWave;
+    float sum = part[0][mb][n][i][l];
 #pragma unroll
-    for (int w = 1; w < kBatchWaves; ++w) sum += part[w][n][i][l];
-    const int e = 16 * n + l % 16, row = 4 * (l / 16) + i;
+    for (int w = 1; w < kBatchWaves; ++w) sum += part[w][mb][n][i][l];
+    const int e = 16 * n + l % 16, row = 16 * mb + 4 * (l / 16) + i;
     const uint32_t h = f32_to_bf16(sum);
     logit[row][e] = bf16_to_f32(h);
     if (logits_out && e < experts) logits_out[(row0 + row) * experts + e] = (bf16)h;
