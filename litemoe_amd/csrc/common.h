@@ -46,6 +46,11 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return f != f ? 0x7fc0u : h;
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+// round_bf16 without the NaN canonicalization, for an intermediate whose NaN
+// (if any) reaches a canonicalizing conversion before anything is stored.
+__device__ __forceinline__ float round_bf16_nc(float f) {
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f) << 16);
+}
 
 // Eight bf16 (one 16-byte word) to floats.
 __device__ __forceinline__ void unpack8(const u32x4 &w, float *f) {
@@ -127,7 +132,13 @@ __device__ __forceinline__ float dot8_bf16_acc(const u32x4 &a, const u32x4 &b, f
   return acc;
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+// x * sigmoid(x) from the hardware exp2 and reciprocal (each within one ulp;
+// the product is within a few fp32 ulps of x / (1 + e^-x), far below the
+// bf16 rounding every caller applies next). Large negative x gives -0 where
+// e^-x overflows; +-inf and NaN behave as in x * sigmoid(x).
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
 
 // MFMA 16x16x32 bf16 (gfx950). Lane l supplies row l%16 of A and column l%16
 // of B, each with the eight k values of k-group l/16; it receives C rows

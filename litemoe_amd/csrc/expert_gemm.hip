@@ -47,33 +47,53 @@ constexpr int kRowBytes = kBK * 2;  // 128
 // or two LDS stages. Measured at 65k tokens (3B shape): 128 x 128 with one
 // LDS stage (33 KB, three workgroups per CU) 3.34 ms for the MoE; with two
 // stages (two per CU) 3.83 ms; 256 x 256 (one per CU, accumulators in AGPRs)
-// 4.16 ms. More waves per CU beat the lower LDS and L2 traffic per MFMA of
-// the larger tile.
-#ifndef LM_EXPERT_GEMM_TILE
-#define LM_EXPERT_GEMM_TILE 128
+// 4.16 ms. At cfg 4 (47k tokens) 256 x 128 on eight waves (the same 64 x 64
+// wave tiles, one workgroup per CU) 2.79 against 2.52 ms; four workgroups per
+// CU of 128 x 128 need 128 registers and spill. More waves per CU beat the
+// lower LDS and L2 traffic per MFMA of the larger tile.
+#ifndef LM_EXPERT_GEMM_TM
+#define LM_EXPERT_GEMM_TM 128
+#endif
+#ifndef LM_EXPERT_GEMM_TN
+#define LM_EXPERT_GEMM_TN 128
 #endif
 #ifndef LM_EXPERT_GEMM_LDS_STAGES
 #define LM_EXPERT_GEMM_LDS_STAGES 1
 #endif
-constexpr int kTile = LM_EXPERT_GEMM_TILE;
+constexpr int kTileM = LM_EXPERT_GEMM_TM, kTileN = LM_EXPERT_GEMM_TN;
 constexpr int kLdsStages = LM_EXPERT_GEMM_LDS_STAGES;
 
 // Block b of the per-expert blocks of bm routes (offsets: exclusive prefix
-// of per-expert counts, as lm_moe_align writes it).
+// of per-expert counts, as lm_moe_align writes it), found by each wave with
+// one vector load per 64 experts: lane l takes expert e0 + l's block count,
+// an inclusive prefix sum over the lanes gives each expert's first block, and
+// the expert holding b is the one lane whose block range contains it. (A
+// scalar walk over the experts waits on one load per expert.)
 __device__ __forceinline__ bool block_of(const int32_t *__restrict__ offsets, int experts, int bm,
                                          int b, int &e_out, int &r0, int &r1) {
-  int o0 = offsets[0];
-  for (int e = 0; e < experts; ++e) {
-    const int o1 = offsets[e + 1];
+  const int lane = threadIdx.x % kWave;
+  int before = 0;  // blocks of the experts below e0
+  for (int e0 = 0; e0 < experts; e0 += kWave) {
+    const int e = e0 + lane;
+    const int o0 = e < experts ? offsets[e] : 0;
+    const int o1 = e < experts ? offsets[e + 1] : 0;
     const int nb = (o1 - o0 + bm - 1) / bm;
-    if (b < nb) {
-      e_out = e;
-      r0 = o0 + b * bm;
-      r1 = min(o1, r0 + bm);
+    int incl = nb;
+#pragma unroll
+    for (int d = 1; d < kWave; d *= 2) {
+      const int up = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += up;
+    }
+    const int first = before + incl - nb;
+    const uint64_t hit = __ballot(b >= first && b < first + nb);
+    if (hit) {
+      const int l = __ffsll((unsigned long long)hit) - 1;
+      e_out = e0 + l;
+      r0 = __shfl(o0, l, kWave) + (b - __shfl(first, l, kWave)) * bm;
+      r1 = min(__shfl(o1, l, kWave), r0 + bm);
       return true;
     }
-    b -= nb;
-    o0 = o1;
+    before += __shfl(incl, kWave - 1, kWave);
   }
   return false;
 }
@@ -97,7 +117,8 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
                    const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
                    int topk, int K, int out_cols, int inter, int experts,
                    bf16 *__restrict__ out) {
-  constexpr int kRB = kTM / 32, kCB = kTN / 32;  // 16-row / 16-column blocks per wave
+  constexpr int kWaveRows = kTM / 2;             // rows of a wave's tile
+  constexpr int kRB = kWaveRows / 16, kCB = kTN / 32;  // 16-row / 16-column blocks per wave
   constexpr int kLA = kTM / 32, kLB = kTN / 32;  // 16-byte loads per lane per operand
   constexpr int kABytes = kTM * kRowBytes, kStageBytes = (kTM + kTN) * kRowBytes;
   __shared__ __align__(16) char smem[kStages * kStageBytes];
@@ -190,9 +211,10 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) {
         const u32x4 af =
-            *reinterpret_cast<const u32x4 *>(as + frag_offset(wr * (kTM / 2) + rb * 16 + fr, kk * 4 + fk));
+            *reinterpret_cast<const u32x4 *>(as + frag_offset(wr * kWaveRows + rb * 16 + fr, kk * 4 + fk));
+        // weights as the first operand: the tile is computed transposed
 #pragma unroll
-        for (int cb = 0; cb < kCB; ++cb) acc[rb][cb] = mfma16x16x32(af, bfr[cb], acc[rb][cb]);
+        for (int cb = 0; cb < kCB; ++cb) acc[rb][cb] = mfma16x16x32(bfr[cb], af, acc[rb][cb]);
       }
     }
   };
@@ -216,25 +238,31 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   }
   compute(kStages == 2 ? (nk - 1) & 1 : 0);
 
-  // C fragment: lane holds rows 4*(lane/16) + i of column lane%16.
+  // Transposed C fragment: lane holds output row lane%16 of each 16-row block
+  // and its output columns 4*(lane/16) .. +3 of each 16-column block, written
+  // as one 8-byte word. Intermediate roundings skip the NaN canonicalization
+  // (a NaN stays NaN through silu and the product, and the stored value is
+  // canonicalized).
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) {
+    const int row = wr * kWaveRows + rb * 16 + fr;
+    if (row >= n) continue;
+    const int64_t orow = kGateUp && kSortedAct ? r0 + row : route_of[row];
+    bf16 *o = out + orow * out_cols + c0 + 4 * fk;
+    if constexpr (kGateUp) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wr * (kTM / 2) + rb * 16 + 4 * fk + i;
-      if (row >= n) continue;
-      const int64_t orow = kGateUp && kSortedAct ? r0 + row : route_of[row];
-      bf16 *o = out + orow * out_cols + c0;
-      if constexpr (kGateUp) {
+      for (int cb = 0; cb < kCB / 2; ++cb) {
+        float h[4];
 #pragma unroll
-        for (int cb = 0; cb < kCB / 2; ++cb) {
-          const float h = round_bf16(silu(round_bf16(acc[rb][cb][i]))) * round_bf16(acc[rb][cb + kCB / 2][i]);
-          o[wc * (kTN / 4) + cb * 16 + fr] = (bf16)f32_to_bf16(h);
-        }
-      } else {
-#pragma unroll
-        for (int cb = 0; cb < kCB; ++cb) o[wc * (kTN / 2) + cb * 16 + fr] = (bf16)f32_to_bf16(acc[rb][cb][i]);
+        for (int i = 0; i < 4; ++i)
+          h[i] = round_bf16_nc(silu(round_bf16_nc(acc[rb][cb][i]))) * round_bf16_nc(acc[rb][cb + kCB / 2][i]);
+        *reinterpret_cast<uint2 *>(o + wc * (kTN / 4) + cb * 16) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
       }
+    } else {
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb)
+        *reinterpret_cast<uint2 *>(o + wc * (kTN / 2) + cb * 16) =
+            make_uint2(pack_bf16(acc[rb][cb][0], acc[rb][cb][1]), pack_bf16(acc[rb][cb][2], acc[rb][cb][3]));
     }
   }
 }
@@ -245,7 +273,7 @@ bool expert_gemm_ok(int64_t routes, int64_t hidden, int64_t inter, int64_t exper
   // 32-bit element offsets: the gathered rows and the weights stay below 2^31.
   const int64_t rows = std::max(routes, experts * std::max(2 * inter, hidden));
   return routes >= kExpertGemmMinRoutes && hidden % kBK == 0 && inter % kBK == 0 &&
-         (2 * inter) % kTile == 0 && hidden % kTile == 0 &&
+         (2 * inter) % kTileN == 0 && hidden % kTileN == 0 &&
          rows * std::max(hidden, inter) < ((int64_t)1 << 31);
 }
 
@@ -253,11 +281,11 @@ int launch_expert_gemm_gate_up(const bf16 *x, const bf16 *w13, const int32_t *of
                                const int32_t *sorted, int64_t routes, int64_t topk, int64_t hidden,
                                int64_t inter, int64_t experts, bf16 *act, bool packed,
                                bool sorted_act, hipStream_t stream) {
-  const int64_t blocks = align_up(cdiv(routes, kTile) + experts, kXcds);
+  const int64_t blocks = align_up(cdiv(routes, kTileM) + experts, kXcds);
   if (blocks > 65535) return LM_EUNSUPPORTED;
-  const dim3 grid((unsigned)(2 * inter / kTile), (unsigned)blocks);
+  const dim3 grid((unsigned)(2 * inter / kTileN), (unsigned)blocks);
   auto go = [&](auto packed_c, auto sorted_c) {
-    expert_gemm_kernel<true, kTile, kTile, kLdsStages, decltype(packed_c)::value,
+    expert_gemm_kernel<true, kTileM, kTileN, kLdsStages, decltype(packed_c)::value,
                        decltype(sorted_c)::value><<<grid, kThreads, 0, stream>>>(
         x, w13, offsets, sorted, (int)topk, (int)hidden, (int)inter, (int)inter, (int)experts, act);
   };
@@ -276,11 +304,11 @@ int launch_expert_gemm_down(const bf16 *act, const bf16 *w2, const int32_t *offs
                             const int32_t *sorted, int64_t routes, int64_t hidden, int64_t inter,
                             int64_t experts, bf16 *y, bool packed, bool sorted_act,
                             hipStream_t stream) {
-  const int64_t blocks = align_up(cdiv(routes, kTile) + experts, kXcds);
+  const int64_t blocks = align_up(cdiv(routes, kTileM) + experts, kXcds);
   if (blocks > 65535) return LM_EUNSUPPORTED;
-  const dim3 grid((unsigned)(hidden / kTile), (unsigned)blocks);
+  const dim3 grid((unsigned)(hidden / kTileN), (unsigned)blocks);
   auto go = [&](auto packed_c, auto sorted_c) {
-    expert_gemm_kernel<false, kTile, kTile, kLdsStages, decltype(packed_c)::value,
+    expert_gemm_kernel<false, kTileM, kTileN, kLdsStages, decltype(packed_c)::value,
                        decltype(sorted_c)::value><<<grid, kThreads, 0, stream>>>(
         act, w2, offsets, sorted, 1, (int)inter, (int)hidden, (int)inter, (int)experts, y);
   };
