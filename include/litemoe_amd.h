@@ -166,6 +166,25 @@ int lm_flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits,
                         int64_t max_len, int64_t num_splits, void *out,
                         void *workspace, int64_t workspace_bytes, void *stream);
 
+/* lm_flash_decode_qkv with out written in the fragment order that
+ * lm_linear_splitk_frag reads (the o_proj input, litemoe/model.py:73): the
+ * [batch, q_heads*64] output padded to 16*mb rows, mb = the smallest of
+ * 1, 2, 4, 8 with 16*mb >= batch; element (b, k) at
+ *   ((k/32)*mb + b/16)*512 + ((k%32)/8)*128 + (b%16)*8 + k%8.
+ * Padding rows are never written. batch <= 128 (else LM_EUNSUPPORTED); the
+ * same values as lm_flash_decode_qkv. No counterpart in the reference: a
+ * layout of this build's decode step. */
+int lm_flash_decode_qkv_frag(const float *qkv_partials, int64_t qkv_splits,
+                             const void *cos_sin, int64_t table_len,
+                             const int64_t *positions, const uint8_t *active,
+                             void *k_cache, void *v_cache, const int32_t *used,
+                             const int32_t *row_order,
+                             int64_t batch, int64_t q_heads, int64_t kv_heads,
+                             int64_t capacity, int64_t head_dim, float scale,
+                             int64_t max_len, int64_t num_splits, void *out_frag,
+                             void *workspace, int64_t workspace_bytes,
+                             void *stream);
+
 /* Variable-length attention over a packed batch (one row per token):
  * sequence s owns tokens [cu[s], cu[s+1]); token i of it attends keys
  * [0, i] of the same sequence when causal, all of them otherwise.
@@ -339,6 +358,16 @@ int lm_moe_finish(const void *y, const int32_t *ids, const int64_t *order,
 int lm_linear_splitk(const void *a, int64_t lda, const void *weight,
                      int64_t rows, int64_t out_features, int64_t in_features,
                      int64_t splits, float *partials, void *stream);
+
+/* lm_linear_splitk with a in the fragment order of lm_flash_decode_qkv_frag
+ * (rows padded to 16*mb, padding rows read and their outputs dropped): each
+ * A load then reads 1 KB contiguously instead of 16 rows x 64 bytes. Same
+ * partials as lm_linear_splitk on the row-major a, same limits,
+ * in_features % 32 == 0. No counterpart in the reference (the projections of
+ * litemoe/model.py:47-49 and :73 on this build's decode-step layout). */
+int lm_linear_splitk_frag(const void *a_frag, const void *weight, int64_t rows,
+                          int64_t out_features, int64_t in_features,
+                          int64_t splits, float *partials, void *stream);
 
 /* out[m][n] = bf16(sum_s partials[s][m][n]), s ascending; out row stride ldo. */
 int lm_linear_splitk_reduce(const float *partials, int64_t splits, int64_t rows,

@@ -54,9 +54,12 @@ _SIGNATURES = {
                                 _i64, _v],
     "lm_moe_finish_add_rmsnorm": [_v, _v, _v, _v, _v, _f32, _v, _f32, _v, _i64, _i64, _i64, _v],
     "lm_linear_splitk": [_v, _i64, _v, _i64, _i64, _i64, _i64, _v, _v],
+    "lm_linear_splitk_frag": [_v, _v, _i64, _i64, _i64, _i64, _v, _v],
     "lm_linear_splitk_reduce": [_v, _i64, _i64, _i64, _v, _i64, _v],
     "lm_flash_decode_qkv": [_v, _i64, _v, _i64, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64,
                             _f32, _i64, _i64, _v, _v, _i64, _v],
+    "lm_flash_decode_qkv_frag": [_v, _i64, _v, _i64, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64,
+                                 _f32, _i64, _i64, _v, _v, _i64, _v],
     "lm_add_rmsnorm_router_splitk": [_v, _v, _i64, _f32, _v, _f32, _v, _v, _i64, _i64, _i64, _i64,
                                      _i32, _v, _v, _v, _v],
     "lm_decode_prologue": [_v, _v, _v, _v, _f32, _v, _f32, _v, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64,

@@ -106,12 +106,20 @@ __device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s
 
 // G <= 3: four waves per SIMD (two workgroups per CU, <= 128 VGPRs); the KV stream
 // needs both workgroups in flight.
+// Output element (row b, q head hq, channel c): row-major [batch, q_heads*D],
+// or with out_mb > 0 the fragment order of frag_offset_rows (the o_proj
+// split-K projection's A operand).
+__device__ __forceinline__ int64_t out_index(int64_t b, int hq, int c, int q_heads, int out_mb) {
+  return out_mb ? frag_offset_rows(b, (int64_t)hq * kD + c, out_mb)
+                : (b * q_heads + hq) * kD + c;
+}
+
 template <int G, bool kFused>
 __global__ void __launch_bounds__(kThreads, G <= 3 ? 4 : 2)
 decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__restrict__ kc,
               bf16 *__restrict__ vc, const int32_t *__restrict__ used, int q_heads,
               int kv_heads, int64_t capacity, float scale, int max_len, int chunk, int splits,
-              Partial part, QkvIn in, bf16 *__restrict__ out) {
+              Partial part, QkvIn in, bf16 *__restrict__ out, int out_mb) {
   __shared__ float sm_o[kWaves][G][kD];
   __shared__ float sm_m[kWaves][G];
   __shared__ float sm_l[kWaves][G];
@@ -383,7 +391,7 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
     }
     const int hq = h * G + g;
     if (splits == 1) {
-      out[((int64_t)b * q_heads + hq) * kD + c] = (bf16)f32_to_bf16(lsum > 0.f ? o / lsum : 0.f);
+      out[out_index(b, hq, c, q_heads, out_mb)] = (bf16)f32_to_bf16(lsum > 0.f ? o / lsum : 0.f);
     } else {
       const int64_t slot = ((int64_t)b * q_heads + hq) * splits + split;
       part.o[slot * kD + c] = o;
@@ -398,7 +406,7 @@ decode_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, bf16 *__rest
 // grid (q_heads, batch), one thread per channel.
 __global__ void __launch_bounds__(kD)
 decode_combine_kernel(const int32_t *__restrict__ used, int q_heads, int64_t capacity, int max_len,
-                      int chunk, int splits, Partial part, bf16 *__restrict__ out) {
+                      int chunk, int splits, Partial part, bf16 *__restrict__ out, int out_mb) {
   const int hq = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int c = threadIdx.x;
@@ -415,7 +423,7 @@ decode_combine_kernel(const int32_t *__restrict__ used, int q_heads, int64_t cap
     lsum += part.l[base + s] * f;
     o += part.o[(base + s) * kD + c] * f;
   }
-  out[((int64_t)b * q_heads + hq) * kD + c] = (bf16)f32_to_bf16(lsum > 0.f ? o / lsum : 0.f);
+  out[out_index(b, hq, c, q_heads, out_mb)] = (bf16)f32_to_bf16(lsum > 0.f ? o / lsum : 0.f);
 }
 
 int64_t workspace_bytes(int64_t batch, int64_t q_heads, int64_t splits) {
@@ -443,8 +451,8 @@ namespace {
 int launch_decode(const void *q, int64_t qs0, int64_t qs1, void *k_cache, void *v_cache,
                   const int32_t *used, int64_t batch, int64_t q_heads, int64_t kv_heads,
                   int64_t capacity, float scale, int64_t max_len, int64_t num_splits,
-                  const QkvIn &in, void *out, void *workspace, int64_t workspace_bytes_,
-                  void *stream) {
+                  const QkvIn &in, void *out, int out_mb, void *workspace,
+                  int64_t workspace_bytes_, void *stream) {
   const int64_t need = workspace_bytes(batch, q_heads, num_splits);
   if (need > 0 && (!workspace || workspace_bytes_ < need)) return LM_EWORKSPACE;
   const int chunk = (int)align_up(cdiv(max_len, num_splits), 16);
@@ -470,12 +478,12 @@ int launch_decode(const void *q, int64_t qs0, int64_t qs1, void *k_cache, void *
       decode_kernel<GG, true><<<grid, kThreads, 0, s>>>(                                          \
           (const bf16 *)q, qs0, qs1, (bf16 *)k_cache, (bf16 *)v_cache, used, (int)q_heads,        \
           (int)kv_heads, capacity, scale, (int)max_len, chunk, stride_splits, part, in,           \
-          (bf16 *)out);                                                                           \
+          (bf16 *)out, out_mb);                                                                   \
     else                                                                                          \
       decode_kernel<GG, false><<<grid, kThreads, 0, s>>>(                                         \
           (const bf16 *)q, qs0, qs1, (bf16 *)k_cache, (bf16 *)v_cache, used, (int)q_heads,        \
           (int)kv_heads, capacity, scale, (int)max_len, chunk, stride_splits, part, in,           \
-          (bf16 *)out);                                                                           \
+          (bf16 *)out, out_mb);                                                                   \
     break;
     X(1) X(2) X(3) X(4) X(6) X(8)
 #undef X
@@ -485,7 +493,8 @@ int launch_decode(const void *q, int64_t qs0, int64_t qs1, void *k_cache, void *
   LM_CHECK_LAUNCH();
   if (splits > 1) {
     decode_combine_kernel<<<dim3((unsigned)q_heads, (unsigned)batch), kD, 0, s>>>(
-        used, (int)q_heads, capacity, (int)max_len, chunk, stride_splits, part, (bf16 *)out);
+        used, (int)q_heads, capacity, (int)max_len, chunk, stride_splits, part, (bf16 *)out,
+        out_mb);
     LM_CHECK_LAUNCH();
   }
   return LM_OK;
@@ -512,8 +521,31 @@ extern "C" int lm_flash_decode(const void *q, int64_t qs0, int64_t qs1, const vo
   const QkvIn in{nullptr, 0, nullptr, 0, nullptr, nullptr, nullptr};
   return launch_decode(q, qs0, qs1, const_cast<void *>(k_cache), const_cast<void *>(v_cache),
                        used, batch, q_heads, kv_heads, capacity, scale, max_len, num_splits, in,
-                       out, workspace, workspace_bytes_, stream);
+                       out, 0, workspace, workspace_bytes_, stream);
 }
+
+namespace {
+
+int flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits, const void *cos_sin,
+                     int64_t table_len, const int64_t *positions, const uint8_t *active,
+                     void *k_cache, void *v_cache, const int32_t *used, const int32_t *row_order,
+                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
+                     int64_t head_dim, float scale, int64_t max_len, int64_t num_splits, void *out,
+                     bool frag_out, void *workspace, int64_t workspace_bytes_, void *stream) {
+  LM_REQUIRE(decode_args_ok(batch, q_heads, kv_heads, capacity, max_len, num_splits));
+  LM_REQUIRE(qkv_splits >= 1 && table_len > 0);
+  if (head_dim != kD || qkv_splits > kMaxQkvSplits) return LM_EUNSUPPORTED;
+  if (frag_out && batch > 128) return LM_EUNSUPPORTED;
+  if (batch == 0) return LM_OK;
+  LM_REQUIRE(qkv_partials && cos_sin && positions && k_cache && v_cache && used && out);
+  const QkvIn in{qkv_partials, (int)qkv_splits, (const bf16 *)cos_sin, table_len, positions,
+                 active, row_order};
+  return launch_decode(nullptr, 0, 0, k_cache, v_cache, used, batch, q_heads, kv_heads, capacity,
+                       scale, max_len, num_splits, in, out, frag_out ? frag_row_blocks(batch) : 0,
+                       workspace, workspace_bytes_, stream);
+}
+
+}  // namespace
 
 extern "C" int lm_flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits,
                                    const void *cos_sin, int64_t table_len,
@@ -524,13 +556,23 @@ extern "C" int lm_flash_decode_qkv(const float *qkv_partials, int64_t qkv_splits
                                    int64_t capacity, int64_t head_dim, float scale,
                                    int64_t max_len, int64_t num_splits, void *out,
                                    void *workspace, int64_t workspace_bytes_, void *stream) {
-  LM_REQUIRE(decode_args_ok(batch, q_heads, kv_heads, capacity, max_len, num_splits));
-  LM_REQUIRE(qkv_splits >= 1 && table_len > 0);
-  if (head_dim != kD || qkv_splits > kMaxQkvSplits) return LM_EUNSUPPORTED;
-  if (batch == 0) return LM_OK;
-  LM_REQUIRE(qkv_partials && cos_sin && positions && k_cache && v_cache && used && out);
-  const QkvIn in{qkv_partials, (int)qkv_splits, (const bf16 *)cos_sin, table_len, positions,
-                 active, row_order};
-  return launch_decode(nullptr, 0, 0, k_cache, v_cache, used, batch, q_heads, kv_heads, capacity,
-                       scale, max_len, num_splits, in, out, workspace, workspace_bytes_, stream);
+  return flash_decode_qkv(qkv_partials, qkv_splits, cos_sin, table_len, positions, active,
+                          k_cache, v_cache, used, row_order, batch, q_heads, kv_heads, capacity,
+                          head_dim, scale, max_len, num_splits, out, false, workspace,
+                          workspace_bytes_, stream);
+}
+
+extern "C" int lm_flash_decode_qkv_frag(const float *qkv_partials, int64_t qkv_splits,
+                                        const void *cos_sin, int64_t table_len,
+                                        const int64_t *positions, const uint8_t *active,
+                                        void *k_cache, void *v_cache, const int32_t *used,
+                                        const int32_t *row_order, int64_t batch, int64_t q_heads,
+                                        int64_t kv_heads, int64_t capacity, int64_t head_dim,
+                                        float scale, int64_t max_len, int64_t num_splits,
+                                        void *out_frag, void *workspace, int64_t workspace_bytes_,
+                                        void *stream) {
+  return flash_decode_qkv(qkv_partials, qkv_splits, cos_sin, table_len, positions, active,
+                          k_cache, v_cache, used, row_order, batch, q_heads, kv_heads, capacity,
+                          head_dim, scale, max_len, num_splits, out_frag, true, workspace,
+                          workspace_bytes_, stream);
 }

@@ -149,6 +149,19 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4 &a, const u32x4 &b, f3
 
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Activation rows in MFMA A-fragment order (the "_frag" entry points): a
+// [rows, K] bf16 matrix padded to 16*mb rows, mb = frag_row_blocks(rows), is
+// stored as k steps of 32 outermost, then the mb 16-row blocks, then the 64
+// lanes of a v_mfma_f32_16x16x32_bf16 A operand (lane = row%16 + 16*k group)
+// with their 8 consecutive k values. One 64-lane load of 16 bytes then reads
+// 1 KB contiguously instead of 16 rows x 64 bytes.
+__host__ __device__ constexpr inline int frag_row_blocks(int64_t rows) {
+  return rows <= 16 ? 1 : rows <= 32 ? 2 : rows <= 64 ? 4 : 8;
+}
+__host__ __device__ inline int64_t frag_offset_rows(int64_t row, int64_t k, int mb) {
+  return ((k >> 5) * mb + (row >> 4)) * 512 + ((k >> 3) & 3) * 128 + (row & 15) * 8 + (k & 7);
+}
+
 }  // namespace lm
 
 // Launch-status check for the C ABI wrappers.

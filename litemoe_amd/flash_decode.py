@@ -16,6 +16,7 @@ import math
 import torch
 
 from . import _lib
+from .linear import FragRows
 
 
 def default_splits(batch, kv_heads, maximum, target_workgroups=512, min_keys=256, max_splits=16):
@@ -65,14 +66,18 @@ class FlashDecode:
                   _lib.stream(q.device))
         return out
 
-    def fused_qkv(self, partials, cos_sin, positions, active, k, v, scale, used, q_heads, row_order=None):
+    def fused_qkv(self, partials, cos_sin, positions, active, k, v, scale, used, q_heads, row_order=None,
+                  frag_out=False):
         """Attention of one new token per row from the packed QKV projection's
         partials ``[S, B, (Hq + 2 Hkv) * 64]`` (litemoe/model.py:47-71 after
         the projection). Writes the rotated key and the value at
         ``positions[b]`` of ``k``/``v`` (rows with ``active`` false, when
-        given, write nothing) and returns ``[B, Hq, 1, 64]``. ``row_order``
-        (int32 ``[B]``, a permutation of the rows) sets the order in which the
-        rows' workgroups are dispatched; results do not depend on it."""
+        given, write nothing) and returns ``[B, Hq, 1, 64]``, or with
+        ``frag_out`` the same values as a ``[B, Hq*64]``
+        :class:`~litemoe_amd.linear.FragRows` (the o_proj split-K input
+        order). ``row_order`` (int32 ``[B]``, a permutation of the rows) sets
+        the order in which the rows' workgroups are dispatched; results do not
+        depend on it."""
         splits, b, ncols = partials.shape
         hkv = k.shape[1]
         if ncols != (q_heads + 2 * hkv) * 64 or q_heads % hkv or k.shape != v.shape:
@@ -90,12 +95,17 @@ class FlashDecode:
         if active is not None:
             # a bool mask is one byte per row: read it in place (no conversion launch)
             act = (active.view(torch.uint8) if active.dtype == torch.bool else active.to(torch.uint8)).contiguous()
-        out = torch.empty(b, q_heads, 1, 64, device=k.device, dtype=k.dtype)
+        if frag_out:
+            out = FragRows(b, q_heads * 64, k.device)
+            out_ptr = out.data.data_ptr()
+        else:
+            out = torch.empty(b, q_heads, 1, 64, device=k.device, dtype=k.dtype)
+            out_ptr = out.data_ptr()
         if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (b,)):
             raise ValueError("row_order must be an int32 [B] permutation")
-        _lib.call("lm_flash_decode_qkv", partials.data_ptr(), splits, cos_sin.data_ptr(), cos_sin.shape[0],
-                  positions.data_ptr(), _lib.ptr(act), k.data_ptr(), v.data_ptr(), used.data_ptr(),
-                  _lib.ptr(row_order), b,
+        _lib.call("lm_flash_decode_qkv_frag" if frag_out else "lm_flash_decode_qkv", partials.data_ptr(),
+                  splits, cos_sin.data_ptr(), cos_sin.shape[0], positions.data_ptr(), _lib.ptr(act),
+                  k.data_ptr(), v.data_ptr(), used.data_ptr(), _lib.ptr(row_order), b,
                   q_heads, hkv, self.capacity, 64, float(scale), self.maximum, self.splits,
-                  out.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(), _lib.stream(k.device))
+                  out_ptr, self.workspace.data_ptr(), self.workspace.numel(), _lib.stream(k.device))
         return out

@@ -51,6 +51,68 @@ def linear_splitk(a, weight, splits, out=None):
     return out
 
 
+def frag_row_blocks(rows):
+    """16-row blocks of the fragment order for ``rows`` rows: the smallest of
+    1, 2, 4, 8 covering them (the split-K kernel's row-block count)."""
+    if not 1 <= rows <= MAX_ROWS:
+        raise ValueError(f"Fragment order holds 1..{MAX_ROWS} rows, got {rows}")
+    return 1 if rows <= 16 else 2 if rows <= 32 else 4 if rows <= 64 else 8
+
+
+class FragRows:
+    """A bf16 ``[rows, cols]`` matrix in MFMA A-fragment order, the layout
+    ``lm_linear_splitk_frag`` reads and ``lm_flash_decode_qkv_frag`` writes
+    (the decode attention output, o_proj's input): rows padded to ``16 * mb``;
+    element ``(r, k)`` at ``((k//32)*mb + r//16)*512 + ((k%32)//8)*128 +
+    (r%16)*8 + k%8``, so one 64-lane load of 16 bytes reads 1 KB contiguously.
+    Padding rows are never written and only feed outputs that are dropped."""
+
+    def __init__(self, rows, cols, device, data=None):
+        if cols % 32:
+            raise ValueError("Fragment order needs a multiple of 32 columns")
+        self.rows, self.cols, self.mb = rows, cols, frag_row_blocks(rows)
+        size = 16 * self.mb * cols
+        if data is None:
+            data = torch.empty(size, device=device, dtype=torch.bfloat16)
+        elif data.numel() != size or data.dtype != torch.bfloat16 or not data.is_contiguous():
+            raise ValueError("Fragment buffer must be contiguous bf16 of 16*mb*cols elements")
+        self.data = data
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @classmethod
+    def from_rows(cls, a):
+        """The fragment order of a row-major ``[rows, cols]`` matrix (padding rows zero)."""
+        rows, cols = a.shape
+        out = cls(rows, cols, a.device)
+        padded = torch.zeros(16 * out.mb, cols, device=a.device, dtype=torch.bfloat16)
+        padded[:rows] = a
+        out.data.copy_(padded.view(out.mb, 16, cols // 32, 4, 8).permute(2, 0, 3, 1, 4).reshape(-1))
+        return out
+
+    def to_rows(self):
+        """The row-major ``[rows, cols]`` matrix."""
+        c = self.cols // 32
+        return self.data.view(c, self.mb, 4, 16, 8).permute(1, 3, 0, 2, 4).reshape(16 * self.mb, self.cols)[:self.rows]
+
+
+def linear_splitk_frag(a, weight, splits, out=None):
+    """:func:`linear_splitk` with ``a`` a :class:`FragRows` (same partials)."""
+    _lib.require_cuda(a.data, weight, what="projection operands")
+    if weight.dtype != torch.bfloat16 or not weight.is_contiguous() or weight.shape[1] != a.cols:
+        raise ValueError("Split-K projection needs a contiguous BF16 [N, K] weight matching the input")
+    n = weight.shape[0]
+    if out is None:
+        out = torch.empty(splits, a.rows, n, device=a.device, dtype=torch.float32)
+    elif out.shape != (splits, a.rows, n) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("Partials buffer must be contiguous fp32 [splits, rows, out_features]")
+    _lib.call("lm_linear_splitk_frag", a.data.data_ptr(), weight.data_ptr(), a.rows, n, a.cols, splits,
+              out.data_ptr(), _lib.stream(a.device))
+    return out
+
+
 def reduce(partials, out=None):
     """``bf16(sum over slices)``, slices in ascending order."""
     splits, rows, n = partials.shape

@@ -66,6 +66,30 @@ def test_linear_splitk_strided_rows_and_unsupported_shapes():
         linear.linear_splitk(bf((16, 1024)).to(DEV), w, 5)  # 8 k steps do not split in 5
 
 
+@pytest.mark.parametrize("rows", [1, 7, 16, 33, 64, 100, 128])
+@pytest.mark.parametrize("n,k", [(2560, 1536), (1536, 1536), (64, 512)])
+@torch.inference_mode()
+def test_linear_splitk_frag_equals_row_major(rows, n, k):
+    """The fragment-order input gives the row-major kernel's partials, bit for
+    bit (the same MFMA operands in the same order; padding rows dropped)."""
+    a = bf((rows, k), 1.0, 7 * rows + n).to(DEV)
+    w = bf((n, k), 0.02, k + 3).to(DEV)
+    fa = linear.FragRows.from_rows(a)
+    for splits in sorted({s for s in (1, 2, 3, 4, 6, 8) if (k // 128) % s == 0 and (k // 128) // s in (1, 2, 3, 4, 6, 8)}):
+        exp = linear.linear_splitk(a, w, splits)
+        got = linear.linear_splitk_frag(fa, w, splits)
+        assert torch.equal(got, exp)
+    # padding rows are never written in the decode step: NaN there reaches no valid row
+    if rows % 16:
+        mb = fa.mb
+        padded = torch.full((16 * mb, k), float("nan"), device=DEV, dtype=torch.bfloat16)
+        padded[:rows] = a
+        data = padded.view(mb, 16, k // 32, 4, 8).permute(2, 0, 3, 1, 4).contiguous().view(-1)
+        junk = linear.FragRows(rows, k, DEV, data)
+        splits = 1 if k == 512 else 3
+        assert torch.equal(linear.linear_splitk_frag(junk, w, splits), linear.linear_splitk(a, w, splits))
+
+
 def _qkv_case(b, hq, hkv, cap, splits, seed):
     g = torch.Generator().manual_seed(seed)
     ncols = (hq + 2 * hkv) * 64
@@ -206,3 +230,27 @@ def test_bf16_rounding_of_every_float():
         nan = torch.isnan(sample)
         assert torch.equal(got[~nan], ref[~nan]), hex(base)
         assert bool((got[nan] == 0x7FC0).all()), hex(base)
+
+
+@pytest.mark.parametrize("b,hq,hkv,cap,attn_splits,qkv_splits", [
+    (64, 24, 8, 1280, 1, 3), (5, 24, 8, 1024, 4, 3), (100, 16, 8, 300, 1, 2), (33, 24, 8, 512, 2, 3)])
+@torch.inference_mode()
+def test_flash_decode_qkv_frag_output_equals_row_major(b, hq, hkv, cap, attn_splits, qkv_splits):
+    part, cos_sin, pos = _qkv_case(b, hq, hkv, cap, qkv_splits, 3 * b + cap)
+    used = (pos + 1).to(torch.int32)
+    cfg = ModelConfig(num_key_value_heads=hkv, hidden_size=hq * 64, num_attention_heads=hq, num_hidden_layers=1)
+    caches = [KVCache(cfg, b, cap, DEV, torch.bfloat16) for _ in range(2)]
+    caches[0].k.normal_()
+    caches[0].v.normal_()
+    caches[1].k.copy_(caches[0].k)
+    caches[1].v.copy_(caches[0].v)
+    fd = flash_decode.FlashDecode(b, hkv, hq // hkv, cap, DEV, num_splits=attn_splits)
+    exp = fd.fused_qkv(part, cos_sin, pos, None, caches[0].k[0], caches[0].v[0], 0.125, used, hq)
+    got = fd.fused_qkv(part, cos_sin, pos, None, caches[1].k[0], caches[1].v[0], 0.125, used, hq, frag_out=True)
+    assert isinstance(got, linear.FragRows) and (got.rows, got.cols) == (b, hq * 64)
+    assert torch.equal(got.to_rows(), exp.view(b, -1))
+    assert torch.equal(caches[1].k, caches[0].k) and torch.equal(caches[1].v, caches[0].v)
+    # o_proj reads it as it reads the row-major output
+    wo = bf((hq * 64, hq * 64), 0.02, 11).to(DEV)
+    splits = linear.pick_splits(b, hq * 64, hq * 64, max_splits=4)
+    assert torch.equal(linear.linear_splitk_frag(got, wo, splits), linear.linear_splitk(exp.view(b, -1), wo, splits))
