@@ -12,7 +12,11 @@
 // read, ds_read_b64_tr_b16: within each 16-lane group, lanes 4j..4j+3 point
 // at 16 consecutive channels of key row j, and lane p receives channel p of
 // rows 0..3. Online softmax (fp32, exp2 with the scale folded in) per query;
-// P is rounded to bf16 for the MFMA.
+// P is rounded to bf16 for the MFMA. The row sum l is a fifth P.V product with
+// an all-ones V block (the sum of the same bf16 P that O accumulates, in O's
+// lane layout), and the running maximum moves only when a tile raises it by
+// more than kLazy (log2 units): until then p <= 2^kLazy, which bf16 P and the
+// fp32 sums carry as exactly as p <= 1, and O is not rescaled.
 //
 // Reference semantics: litemoe/packed.py:12-16 (aten varlen flash attention,
 // causal, q and k share cu_seqlens).
@@ -26,6 +30,8 @@ constexpr int kThreads = 256;
 constexpr int kBK = 64;
 constexpr int kStage = kBK / 32;  // keys each staging thread loads per tile (one per 32)
 constexpr int kKPad = 8;
+constexpr float kLazy = 8.f;
+constexpr uint32_t kOnes = 0x3F803F80u;  // two bf16 1.0
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
@@ -71,8 +77,8 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
   // Sub-block qs: queries wq0 + 16 qs + (0..15); lane col owns query
   // wq0 + 16 qs + col's softmax state.
   u32x4 qf0[kQS], qf1[kQS];
-  float m[kQS], l[kQS];
-  f32x4 o[kQS][4];
+  float m[kQS];
+  f32x4 o[kQS][4], lsum[kQS];  // lsum: C layout of o, every column the row sum
 #pragma unroll
   for (int qs = 0; qs < kQS; ++qs) {
     const int qi = wq0 + 16 * qs + col;
@@ -83,7 +89,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
       qf1[qs] = *reinterpret_cast<const u32x4 *>(qp + 32);
     }
     m[qs] = -INFINITY;
-    l[qs] = 0.f;
+    lsum[qs] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 4; ++d) o[qs][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -158,41 +164,46 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
         for (int i = 0; i < 4; ++i) mt = fmaxf(mt, st[qs][h][i]);
       mt = fmaxf(mt, xor_lanes<16>(mt));  // the four lane groups hold a query's keys
       mt = fmaxf(mt, xor_lanes<32>(mt));
-      const float mn = fmaxf(m[qs], mt * sl2);
-      const float corr = factor(m[qs], mn);
-      float rs = 0.f;
-#pragma unroll
-      for (int h = 0; h < kH; ++h) {
-        float p[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qs][h][i], sl2, -mn));  // exp2(-inf) = 0; mn is finite
-          rs += p[i];
-        }
-        pw[qs][2 * h] = pack_bf16_finite(p[0], p[1]);  // p = exp2(finite or -inf): never NaN
-        pw[qs][2 * h + 1] = pack_bf16_finite(p[2], p[3]);
-      }
-      rs += xor_lanes<16>(rs);
-      rs += xor_lanes<32>(rs);
-      l[qs] = l[qs] * corr + rs;
-      m[qs] = mn;
-
-      // O rows held by this lane are queries 4*grp + i of the sub-block; the
-      // rescale is skipped when no query of the sub-block moved its maximum.
-      if (__ballot(corr != 1.f)) {
+      // The first tile always sets the maximum (m = -inf; key 0 is visible to
+      // every query); a tile fully masked for a query has mt = -inf and keeps it.
+      const float cand = mt * sl2;
+      const bool raise = cand > m[qs] + kLazy;
+      if (__ballot(raise)) {
+        const float mn = raise ? cand : m[qs];
+        const float corr = factor(m[qs], mn);  // 1 for the queries that keep theirs
+        m[qs] = mn;
+        // O and lsum rows held by this lane are queries 4*grp + i
         float rc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) rc[i] = __shfl(corr, grp * 4 + i, kWave);
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
+        for (int i = 0; i < 4; ++i) {
+          lsum[qs][i] *= rc[i];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o[qs][d][i] *= rc[i];
+          for (int d = 0; d < 4; ++d) o[qs][d][i] *= rc[i];
+        }
+      }
+      const float mq = m[qs];  // finite from the first tile on
+#pragma unroll
+      for (int h = 0; h < kH; ++h) {
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qs][h][i], sl2, -mq));  // exp2(-inf) = 0
+        pw[qs][2 * h] = pack_bf16_finite(p[0], p[1]);  // p = exp2(finite or -inf): never NaN
+        pw[qs][2 * h + 1] = pack_bf16_finite(p[2], p[3]);
       }
     }
     // Each 32 keys of the tile are one P.V step: keys 32c + (the two
     // 16-key blocks' rows) as the eight k slots.
+    constexpr u32x4 kOnesB = {kOnes, kOnes, kOnes, kOnes};
 #pragma unroll
     for (int c = 0; c < kBK / 32; ++c) {
+#pragma unroll
+      for (int qs = 0; qs < kQS; ++qs) {
+        const u32x4 pa = {pw[qs][4 * c], pw[qs][4 * c + 1], pw[qs][4 * c + 2], pw[qs][4 * c + 3]};
+        lsum[qs] = mfma16x16x32(pa, kOnesB, lsum[qs]);
+      }
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const uint2 lo = read_tr(&vs_lds[32 * c + trow][d * 16 + tch]);
@@ -209,9 +220,7 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
   if (!wave_live) return;
 #pragma unroll
   for (int qs = 0; qs < kQS; ++qs) {
-    float rl[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rl[i] = __shfl(l[qs], grp * 4 + i, kWave);
+    const f32x4 rl = lsum[qs];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int qq = wq0 + 16 * qs + grp * 4 + i;
