@@ -55,7 +55,9 @@ __device__ __forceinline__ uint2 read_tr(const bf16 *p) {
 // Per query the arithmetic is the same for every kQS (a tile that is fully
 // masked for one sub-block adds exact zeros to its state).
 template <int kQS>
-__global__ void __launch_bounds__(kThreads)
+// Four waves per SIMD (<= 128 registers; the Q fragments live in LDS for it):
+// 0.350 -> 0.328 ms per layer at cfg 4 against three waves with Q in registers.
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
 prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 *__restrict__ k,
                int64_t ks0, int64_t ks1, const bf16 *__restrict__ v, int64_t vs0, int64_t vs1,
                const int32_t *__restrict__ cu, int q_heads, int kv_heads, float scale, int causal,
@@ -63,6 +65,9 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
   constexpr int kBQ = 64 * kQS;
   __shared__ __attribute__((aligned(16))) bf16 ks_lds[kBK][kD + kKPad];
   __shared__ __attribute__((aligned(16))) bf16 vs_lds[kBK][kD + kKPad];
+  // the workgroup's Q fragments, lane-major (re-read each tile instead of
+  // held in 16 registers: four waves per SIMD fit in 128 registers)
+  __shared__ __attribute__((aligned(16))) u32x4 qs_lds[4][kQS][2][kWave];
   const int qb = blockIdx.x, hq = blockIdx.y, seq = blockIdx.z;
   const int start = cu[seq];
   const int len = cu[seq + 1] - start;
@@ -76,18 +81,19 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
 
   // Sub-block qs: queries wq0 + 16 qs + (0..15); lane col owns query
   // wq0 + 16 qs + col's softmax state.
-  u32x4 qf0[kQS], qf1[kQS];
   float m[kQS];
   f32x4 o[kQS][4], lsum[kQS];  // lsum: C layout of o, every column the row sum
 #pragma unroll
   for (int qs = 0; qs < kQS; ++qs) {
     const int qi = wq0 + 16 * qs + col;
-    qf0[qs] = qf1[qs] = u32x4{0u, 0u, 0u, 0u};
+    u32x4 f0 = u32x4{0u, 0u, 0u, 0u}, f1 = f0;
     if (qi < len) {
       const bf16 *qp = q + (int64_t)(start + qi) * qs0 + (int64_t)hq * qs1 + grp * 8;
-      qf0[qs] = *reinterpret_cast<const u32x4 *>(qp);
-      qf1[qs] = *reinterpret_cast<const u32x4 *>(qp + 32);
+      f0 = *reinterpret_cast<const u32x4 *>(qp);
+      f1 = *reinterpret_cast<const u32x4 *>(qp + 32);
     }
+    qs_lds[wave][qs][0][lane] = f0;  // read back by the same lane only
+    qs_lds[wave][qs][1][lane] = f1;
     m[qs] = -INFINITY;
     lsum[qs] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -128,6 +134,12 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     if (!wave_live || (causal && kt > wq0 + 16 * kQS - 1)) continue;
     constexpr int kH = kBK / 16;  // 16-key blocks of the tile
     f32x4 st[kQS][kH];
+    u32x4 qf0[kQS], qf1[kQS];
+#pragma unroll
+    for (int qs = 0; qs < kQS; ++qs) {
+      qf0[qs] = qs_lds[wave][qs][0][lane];
+      qf1[qs] = qs_lds[wave][qs][1][lane];
+    }
 #pragma unroll
     for (int h = 0; h < kH; ++h) {
       const u32x4 a0 = *reinterpret_cast<const u32x4 *>(&ks_lds[16 * h + col][grp * 8]);
