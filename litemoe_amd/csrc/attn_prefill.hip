@@ -150,19 +150,28 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
         st[qs][h] = mfma16x16x32(a1, qf1[qs], st[qs][h]);
       }
     }
-    // Only a tile past the sequence end or crossing the causal diagonal of
-    // this wave's queries has masked scores.
-    const bool masking = kt + kBK > len || (causal && kt + kBK - 1 > wq0);
-    if (masking) {
+    // Only a tile crossing the causal diagonal of this wave's queries, or the
+    // sequence's last tile, has masked scores. Key j = kt + 16h + 4grp + i
+    // against query q = wq0 + 16qs + col: j - q = base + 16(h - qs) + i.
+    if (causal && kt + kBK - 1 > wq0) {
+      const int base = kt - wq0 + 4 * grp - col;
 #pragma unroll
       for (int qs = 0; qs < kQS; ++qs)
 #pragma unroll
         for (int h = 0; h < kH; ++h)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int j = kt + 16 * h + grp * 4 + i;
-            if (j >= len || (causal && j > wq0 + 16 * qs + col)) st[qs][h][i] = -INFINITY;
-          }
+          for (int i = 0; i < 4; ++i)
+            if (base + 16 * (h - qs) + i > 0) st[qs][h][i] = -INFINITY;
+    }
+    if (kt + kBK > len) {
+      const int room = len - kt - 4 * grp;  // j < len  <=>  16h + i < room
+#pragma unroll
+      for (int qs = 0; qs < kQS; ++qs)
+#pragma unroll
+        for (int h = 0; h < kH; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (16 * h + i >= room) st[qs][h][i] = -INFINITY;
     }
     uint32_t pw[kQS][2 * kH];
 #pragma unroll
