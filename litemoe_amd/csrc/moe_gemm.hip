@@ -303,6 +303,46 @@ gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
   };
   if (n <= 16) {
     block(0);
+  } else if (kPacked && n <= 32) {
+    // (fragment-order weights: the checkpoint-layout variant would spill)
+    // Two row blocks in one pass over K: each weight fragment feeds both
+    // blocks' MFMAs and is then dead, as in the one-block case, so the
+    // second block's activations stream in behind the MFMAs instead of
+    // waiting for the first block's reduction. Per row the same MFMAs in the
+    // same order: the same bits as two passes.
+    const bf16 *xr0 = x + (int64_t)(list[col] / topk) * hidden + kbase;
+    const bf16 *xr1 = x + (int64_t)(list[min(16 + col, n - 1)] / topk) * hidden + kbase;
+    f32x4 cg0 = {0.f, 0.f, 0.f, 0.f}, cu0 = cg0, cg1 = cg0, cu1 = cg0;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 a0 = load16(xr0 + s * 32), a1 = load16(xr1 + s * 32);
+      cg0 = mfma16x16x32(a0, bg[s], cg0);
+      cu0 = mfma16x16x32(a0, bu[s], cu0);
+      cg1 = mfma16x16x32(a1, bg[s], cg1);
+      cu1 = mfma16x16x32(a1, bu[s], cu1);
+    }
+    f32x4 cg[2] = {cg0, cg1}, cu[2] = {cu0, cu1};
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        red[wave][0][i][lane] = cg[hb][i];
+        red[wave][1][i][lane] = cu[hb][i];
+      }
+      __syncthreads();
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        g += red[w][0][wave][lane];
+        u += red[w][1][wave][lane];
+      }
+      const int row = 16 * hb + grp * 4 + wave;
+      if (row < n) {
+        const float h = round_bf16(silu(round_bf16(g))) * round_bf16(u);
+        act[(int64_t)list[row] * inter + n0 + col] = (bf16)f32_to_bf16(h);
+      }
+      __syncthreads();
+    }
   } else {
     for (int rb = 0; rb < n; rb += 16) block(rb);
   }
