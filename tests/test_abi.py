@@ -53,6 +53,11 @@ def test_workspace_queries():
     (lambda h: h.lm_fused_experts(None, None, None, None, None, None, 4, 1000, 512, 8, 2, 0, None, None, 0, None), 2),
     (lambda h: h.lm_moe_finish(None, None, None, None, None, None, 1, 8, 9, 0, 1, None, 0, None), 1),
     (lambda h: h.lm_router(None, None, 2, 1536, 300, 8, 1, None, None, None, None), 2),
+    # fragment-order entry points: more than 128 rows, K not a multiple of 32
+    (lambda h: h.lm_linear_splitk_frag(None, None, 129, 512, 1024, 2, None, None), 2),
+    (lambda h: h.lm_linear_splitk_frag(None, None, 4, 512, 1000, 2, None, None), 1),
+    (lambda h: h.lm_flash_decode_qkv_frag(None, 3, None, 16, None, None, None, None, None, None, 200, 24, 8,
+                                          1024, 64, C.c_float(1.0), 1024, 1, None, None, 0, None), 2),
 ])
 def test_invalid_arguments_rejected_on_host(call, expected):
     assert call(_lib.load()) == expected
