@@ -24,8 +24,8 @@ Also reported on the same JSON line:
   engine_decode_tps  the reference's own metric from Engine.generate()
                 (decode_tokens / decode_s with the async output ring).
 
-Two other workloads of the survey's measurement table print their own JSON
-line (not the driver's decode line):
+Two other benchmark configurations print their own JSON line (not the
+driver's decode line):
   --prefill       cfg 4: packed prefill of 48 prompts, lengths U{64..2048}
                   (seed 2), on the 3B shape: prefill tok/s, and the MFMA
                   utilisation of the prefill MoE (uniform routes and 50% of

@@ -2,7 +2,7 @@
 
 * cfg 4: packed ragged prefill of 48 prompts, lengths U{64..2048} (seed 2,
   about 47k tokens), on the Granite-3B shape (two layers) with four hot
-  experts taking about half of the routes. The skew is the survey's recipe:
+  experts taking about half of the routes. The skew is made this way:
   a constant vector c is added to every embedding row and beta * c/|c| to
   the router rows of four hot experts, beta calibrated here so that layer 0
   sends 45-55% of its routes to them. Checked at the full token count:
