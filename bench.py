@@ -103,6 +103,7 @@ def moe_roofline(model, cfg, batch, reps):
     import torch
 
     from litemoe_amd import _lib, experts, router
+    from litemoe_amd.execution import no_collection_while_recording
     dev = model.w["embedding"].device
     H, I, E, k = cfg.hidden_size, cfg.intermediate_size, cfg.num_local_experts, cfg.num_experts_per_tok
     gen = torch.Generator(device=dev).manual_seed(7)
@@ -144,7 +145,7 @@ def moe_roofline(model, cfg, batch, reps):
         with torch.cuda.stream(side):
             fn()  # workspaces allocated outside the recording
             side.synchronize()
-            with torch.cuda.graph(graph, stream=side):
+            with no_collection_while_recording(), torch.cuda.graph(graph, stream=side):
                 fn()
         torch.cuda.current_stream().wait_stream(side)
         graph.replay()

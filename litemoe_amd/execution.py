@@ -21,7 +21,9 @@ the reference's counterpart; its contract is kept, its mechanism is not):
   returns, i.e. before the step that writes that slot again is queued; the
   host runs at most ``depth - 1`` steps ahead of the device.
 """
+import contextlib
 import ctypes
+import gc
 from collections import deque
 
 import torch
@@ -37,6 +39,23 @@ class StepGraph:
 
     def replay(self):
         self.graph.replay()
+
+
+@contextlib.contextmanager
+def no_collection_while_recording():
+    """Around a HIP graph recording: dead Python cycles (a finished engine's
+    pinned output ring and its events, say) are freed before it, and no
+    automatic collection runs inside it. Their destructors make runtime calls
+    that a global-mode capture forbids, and an error raised there aborts the
+    process. (This torch build collects before a capture only when asked to.)"""
+    gc.collect()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if enabled:
+            gc.enable()
 
 
 def capture_decode(step, reset, warmups=2, pool=None):
@@ -60,8 +79,9 @@ def capture_decode(step, reset, warmups=2, pool=None):
             step()
         reset()
         stream.synchronize()
-        with torch.cuda.graph(graph, pool=pool, stream=stream):
-            step()
+        with no_collection_while_recording():
+            with torch.cuda.graph(graph, pool=pool, stream=stream):
+                step()
     caller.wait_stream(stream)
     reset()
     torch.cuda.synchronize(caller.device)
