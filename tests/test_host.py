@@ -155,3 +155,36 @@ def test_workspace_growth_keeps_handed_out_buffers():
     del small
     assert any(buf.data_ptr() == address for buf in ws.retired)
     assert ws.get("cpu", 5000) is large
+
+
+def test_graph_recording_runs_with_the_collector_off():
+    """A recording starts after a collection and runs with automatic
+    collection off (a dead cycle freed mid-capture could make a forbidden
+    runtime call); the collector's state is restored, also on an error."""
+    import gc
+
+    from litemoe_amd.execution import no_collection_while_recording
+
+    class Cycle:
+        def __init__(self):
+            self.me = self
+
+    freed = []
+    Cycle.__del__ = lambda self: freed.append(1)
+    Cycle()  # unreachable, kept alive only by its cycle
+    assert gc.isenabled()
+    with no_collection_while_recording():
+        assert freed == [1]  # collected before the recording starts
+        assert not gc.isenabled()
+    assert gc.isenabled()
+    with pytest.raises(RuntimeError):
+        with no_collection_while_recording():
+            raise RuntimeError("capture failed")
+    assert gc.isenabled()
+    gc.disable()
+    try:
+        with no_collection_while_recording():
+            assert not gc.isenabled()
+        assert not gc.isenabled()  # a caller that had it off keeps it off
+    finally:
+        gc.enable()
