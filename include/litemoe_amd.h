@@ -191,8 +191,11 @@ int lm_flash_decode_qkv_frag(const float *qkv_partials, int64_t qkv_splits,
  * Replaces litemoe/packed.py:12-16 (`PackedPrefill.attention` ->
  * `aten._flash_attention_forward(q, k, v, cu, cu, max, max, 0.0, causal=True,
  * False, scale)`). q: [tokens, q_heads, 64], k/v: [tokens, kv_heads, 64] with
- * row/head strides, channels contiguous; out: [tokens, q_heads, 64]
- * contiguous bf16; cu: int32 [num_seqs + 1]; max_len bounds every sequence. */
+ * row/head strides (multiples of 8 elements), channels contiguous; out:
+ * [tokens, q_heads, 64] contiguous bf16; q, k, v and out 16-byte aligned
+ * (LM_EINVAL otherwise); cu: int32 [num_seqs + 1]; max_len bounds every
+ * sequence. O / l is O times the hardware reciprocal of l (within one fp32 ulp
+ * of the division before the bf16 rounding). */
 int lm_prefill_attention(const void *q, int64_t qs0, int64_t qs1,
                          const void *k, int64_t ks0, int64_t ks1,
                          const void *v, int64_t vs0, int64_t vs1,

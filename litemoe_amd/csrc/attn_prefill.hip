@@ -239,18 +239,41 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
     }
   }
   if (!wave_live) return;
+  // O / l, written through the wave's own Q staging area (2 KB per sub-block:
+  // its 16 * kQS output rows of 128 bytes; only this wave uses it, and the
+  // fence below keeps its last Q reads ahead of these writes), then read back
+  // row-contiguous so every row leaves as eight 16-byte stores instead of 64
+  // 2-byte ones. The 16-byte chunk c of row r sits at c ^ 2((r / 4) % 4): the
+  // four lane groups of one write (rows 4 apart) then hit different banks.
+  // l >= 1 for every query that has a key (its maximum key has p >= 1), and
+  // the reciprocal (within one ulp) times O replaces a division per output.
+  uint16_t *tile = reinterpret_cast<uint16_t *>(qs_lds[wave]);
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
   for (int qs = 0; qs < kQS; ++qs) {
-    const f32x4 rl = lsum[qs];
+    float r[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int qq = wq0 + 16 * qs + grp * 4 + i;
-      if (qq >= len) continue;
-      bf16 *op = out + ((int64_t)(start + qq) * q_heads + hq) * kD;
+    for (int i = 0; i < 4; ++i) r[i] = lsum[qs][i] > 0.f ? __builtin_amdgcn_rcpf(lsum[qs][i]) : 0.f;
 #pragma unroll
-      for (int d = 0; d < 4; ++d)
-        op[d * 16 + col] = (bf16)f32_to_bf16(rl[i] > 0.f ? o[qs][d][i] / rl[i] : 0.f);
+    for (int d = 0; d < 4; ++d) {
+      const int chunk = (2 * d + col / 8) ^ (2 * grp);  // rows 16 qs + 4 grp + i: (r / 4) % 4 = grp
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const uint32_t w = pack_bf16(o[qs][d][i] * r[i], o[qs][d][i + 1] * r[i + 1]);
+        const int at = (16 * qs + 4 * grp + i) * 64 + chunk * 8 + col % 8;
+        tile[at] = (uint16_t)w;
+        tile[at + 64] = (uint16_t)(w >> 16);
+      }
     }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  const u32x4 *rows = reinterpret_cast<const u32x4 *>(tile);
+#pragma unroll
+  for (int j = 0; j < 2 * kQS; ++j) {
+    const int row = 8 * j + lane / 8, c = lane % 8;
+    const u32x4 val = rows[row * 8 + (c ^ (2 * ((row / 4) % 4)))];
+    if (wq0 + row < len)
+      *reinterpret_cast<u32x4 *>(out + ((int64_t)(start + wq0 + row) * q_heads + hq) * kD + c * 8) = val;
   }
 }
 
@@ -270,6 +293,11 @@ extern "C" int lm_prefill_attention(const void *q, int64_t qs0, int64_t qs1, con
   if (head_dim != kD) return LM_EUNSUPPORTED;
   if (num_seqs == 0 || tokens == 0 || max_len == 0) return LM_OK;
   LM_REQUIRE(q && k && v && cu_seqlens && out);
+  // 16-byte loads of q/k/v rows and 16-byte stores of output rows.
+  const auto aligned = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+  LM_REQUIRE(aligned(q) && aligned(k) && aligned(v) && aligned(out));
+  LM_REQUIRE(qs0 % 8 == 0 && qs1 % 8 == 0 && ks0 % 8 == 0 && ks1 % 8 == 0 && vs0 % 8 == 0 &&
+             vs1 % 8 == 0);
 // Two sub-blocks per wave: 0.46 -> 0.41 ms per layer at cfg 4 with the
 // accumulators in VGPRs (built that way); in the AGPR form the second
 // sub-block costs occupancy and is slower than one.

@@ -109,6 +109,12 @@ _P = 16
     ("pack aliasing", lambda h: h.lm_expert_pack(_P, _P + 4096, 8, 1024, 512, _P, _P + 8192, None), 1),
     ("pack misaligned", lambda h: h.lm_expert_pack(_P + 2, _P + 4096, 8, 1024, 512, _P + 8192, _P + 16384, None),
      1),
+    ("prefill out misaligned", lambda h: h.lm_prefill_attention(_P, 2560, 64, _P, 2560, 64, _P, 2560, 64, _P, 2,
+                                                                  128, 64, 24, 8, 64, C.c_float(0.125), 1, _P + 2,
+                                                                  None), 1),
+    ("prefill q stride 2564", lambda h: h.lm_prefill_attention(_P, 2564, 64, _P, 2560, 64, _P, 2560, 64, _P, 2,
+                                                                 128, 64, 24, 8, 64, C.c_float(0.125), 1, _P, None),
+     1),
     ("routes packed workspace short", lambda h: h.lm_moe_routes_packed(_P, _P, _P, _P, 64, 1536, 512, 40, 8, 0, _P,
                                                                          _P, 4096, None), 4),
     ("ok: zero tokens", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 0, 1024, 512, 8, 2, 0, _P, _P, 0,
