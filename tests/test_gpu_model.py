@@ -175,6 +175,16 @@ def test_granite_1b_shape_layer_graph_replay_is_deterministic():
         assert run_g.generate()[0] == eager
 
 
+def _cache_difference(part, mode, got, exp):
+    """Where two KV caches [layers, rows, kv heads, positions, 64] differ."""
+    ne = got.view(torch.int16) != exp.view(torch.int16)
+    layers = ne.flatten(1).any(1).nonzero().flatten().tolist()
+    positions = ne.any(4).any(2).any(1).any(0).nonzero().flatten().tolist()
+    rows = ne.any(4).any(3).any(2).any(0).nonzero().flatten().tolist()
+    return (f"{mode}: cache.{part} differs in {int(ne.sum())} elements; layers {layers[:8]}, "
+            f"rows {rows[:8]} ({len(rows)}), positions {positions[:4]}..{positions[-4:]}")
+
+
 @pytest.mark.parametrize("name,batch,lengths,capacity", [
     ("granite-3b", 64, 1024, 2048),                   # cfg 3, the headline configuration
     ("granite-1b", 32, 512, 1024),                    # cfg 2
@@ -208,8 +218,9 @@ def test_full_size_graph_replay_equals_eager(name, batch, lengths, capacity):
             assert metrics["output_tokens"] == batch * 5
             for k in eager_run.state:
                 assert torch.equal(graph_run.state[k], eager_run.state[k]), k
-            assert torch.equal(graph_run.cache.k, eager_run.cache.k)
-            assert torch.equal(graph_run.cache.v, eager_run.cache.v)
+            for part in ("k", "v"):
+                got, exp = getattr(graph_run.cache, part), getattr(eager_run.cache, part)
+                assert torch.equal(got, exp), _cache_difference(part, mode, got, exp)
         del graph_run
     del eager_run, model, w
     torch.cuda.empty_cache()
