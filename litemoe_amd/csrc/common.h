@@ -41,6 +41,9 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 __device__ __forceinline__ uint32_t pack_bf16_finite(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
+// pack_bf16 without the NaN canonicalization, for intermediates whose NaN (if
+// any) reaches a canonicalizing conversion before anything is stored.
+__device__ __forceinline__ uint32_t pack_bf16_nc(float lo, float hi) { return pack_bf16_finite(lo, hi); }
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   const uint32_t h = __builtin_bit_cast(uint16_t, (__bf16)f);
   return f != f ? 0x7fc0u : h;

@@ -133,6 +133,9 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
     wv[v] = reinterpret_cast<const u32x4 *>(w)[i];
   }
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
+  // Intermediate roundings skip the NaN fix-up: a NaN term makes its sum, x
+  // and z NaN whatever the payload, and x and z are stored through pack_bf16,
+  // so the stored bits are those of the canonicalizing form.
   // Every thread of the workgroup combines the same token, so its route
   // keys (logical id, branch) are uniform: read from their lanes into scalar
   // registers, ranked with scalar work, and the ordered sum branches
@@ -168,12 +171,12 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
 #pragma unroll
       for (int j = 0; j < kMaxK; ++j) {
         if (order[j] == q) {  // uniform
-          const float s = round_bf16(sc[j]);
+          const float s = round_bf16_nc(sc[j]);
           float f[8];
           unpack8(yv[v][j], f);
           u32x4 p;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) p[c] = pack_bf16(f[2 * c] * s, f[2 * c + 1] * s);
+          for (int c = 0; c < 4; ++c) p[c] = pack_bf16_nc(f[2 * c] * s, f[2 * c + 1] * s);
           float term[8];
           unpack8(p, term);
 #pragma unroll
@@ -191,7 +194,7 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
     u32x4 o;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      xn[v][c] = round_bf16(xf[c] + alpha * round_bf16(total[c]));
+      xn[v][c] = round_bf16_nc(xf[c] + alpha * round_bf16_nc(total[c]));
       ss += xn[v][c] * xn[v][c];
     }
 #pragma unroll
@@ -211,8 +214,8 @@ finish_add_norm_kernel(const bf16 *__restrict__ y, const int32_t *__restrict__ i
     u32x4 o;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      o[c] = pack_bf16(round_bf16(xn[v][2 * c] * scale) * g[2 * c],
-                       round_bf16(xn[v][2 * c + 1] * scale) * g[2 * c + 1]);
+      o[c] = pack_bf16(round_bf16_nc(xn[v][2 * c] * scale) * g[2 * c],
+                       round_bf16_nc(xn[v][2 * c + 1] * scale) * g[2 * c + 1]);
     reinterpret_cast<u32x4 *>(z + t * hidden)[i] = o;
   }
 }

@@ -381,6 +381,8 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
   }
   u32x4 w[F::kBatch][NV];
   load_gate_round<NV>(wr, experts, 0, w);
+  // Intermediate roundings below skip the NaN fix-up: x and z leave through
+  // pack_bf16 (canonical NaN), and z reaches the logits only as those bits.
   float xn[NN][8];
   if (norm_wave) {
     float ss = 0.f;
@@ -401,15 +403,15 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
           }
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
-            g[c] = round_bf16(lo[c]);
-            g[4 + c] = round_bf16(hi[c]);
+            g[c] = round_bf16_nc(lo[c]);
+            g[4 + c] = round_bf16_nc(hi[c]);
           }
         } else {
           unpack8(av[v], g);
         }
         u32x4 o;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) xn[v][c] = round_bf16(xn[v][c] + alpha * g[c]);
+        for (int c = 0; c < 8; ++c) xn[v][c] = round_bf16_nc(xn[v][c] + alpha * g[c]);
 #pragma unroll
         for (int c = 0; c < 4; ++c) o[c] = pack_bf16(xn[v][2 * c], xn[v][2 * c + 1]);
         xr[i] = o;
@@ -443,8 +445,8 @@ fast_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha
         u32x4 o;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-          o[c] = pack_bf16(round_bf16(xn[v][2 * c] * scale) * g[2 * c],
-                           round_bf16(xn[v][2 * c + 1] * scale) * g[2 * c + 1]);
+          o[c] = pack_bf16(round_bf16_nc(xn[v][2 * c] * scale) * g[2 * c],
+                           round_bf16_nc(xn[v][2 * c + 1] * scale) * g[2 * c + 1]);
         zs[i] = o;
         zr[i] = o;
       }
