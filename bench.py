@@ -244,6 +244,17 @@ def prefill_bench(args):
         cu = torch.cat((ends.new_zeros(1), ends)).to(dev)
         ms = hip_time(lambda: packed.varlen_attention(q, kk, vv, cu, max(lengths), cfg.attention_multiplier), 5)
         attn_flops = sum(n * (n + 1) // 2 for n in lengths) * hq * 4 * d
+        # The dense projections (lm_linear) beside torch's F.linear (hipBLASLt) on the same operands.
+        from litemoe_amd.linear import linear_dense
+        projections = {}
+        for name, weight in (("qkv", layer["self_attn.qkv_proj"]), ("o_proj", layer["self_attn.o_proj"])):
+            out = torch.empty(tokens, weight.shape[0], device=dev, dtype=torch.bfloat16)
+            own = hip_time(lambda: linear_dense(z, weight, out=out), 5)
+            blas = hip_time(lambda: torch.nn.functional.linear(z, weight), 5)
+            flops = 2 * tokens * H * weight.shape[0]
+            projections[name] = {"ms": round(own, 4), "frac": round(flops / own / 1e9 / BF16_PEAK_TFLOPS, 4),
+                                 "hipblaslt_ms": round(blas, 4),
+                                 "hipblaslt_frac": round(flops / blas / 1e9 / BF16_PEAK_TFLOPS, 4)}
     line = {
         "metric": "prefill tok/s, Granite-3B-shape bf16, cfg4 packed prefill", "value": round(tokens / elapsed, 1),
         "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
@@ -251,6 +262,7 @@ def prefill_bench(args):
         "config": {"workload": f"cfg4 packed prefill: {args.model} shape, 48 prompts, {tokens} tokens",
                    "tokens": tokens, "ms": round(elapsed * 1e3, 2)},
         "moe_mfma": {"flops_per_layer": moe_flops, "peak_tflops": BF16_PEAK_TFLOPS, **moe},
+        "projections_mfma": projections,
         "attention_mfma": {"flops_per_layer": attn_flops, "ms_per_layer": round(ms, 3),
                            "tflops": round(attn_flops / ms / 1e9, 1),
                            "frac": round(attn_flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4)},

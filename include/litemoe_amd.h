@@ -377,6 +377,24 @@ int lm_linear_splitk_reduce(const float *partials, int64_t splits, int64_t rows,
                             int64_t out_features, void *out, int64_t ldo,
                             void *stream);
 
+/* ------------------------------------------------- dense projections -- */
+
+/* Dense projection for any row count:
+ *   out[m][n] = bf16( sum_k a[m][k] * weight[n][k] )   (fp32 accumulation)
+ * Each output is reduced by one workgroup over all of K in ascending 32-wide
+ * k steps, so a row's result is the same bits whatever the row count, the
+ * row's position or the launch (no split-K, no atomics). Replaces the
+ * F.linear calls of the packed prefill and of decode batches above 128 rows:
+ * litemoe/model.py:47-49 (packed q|k|v), :60 and :73 (o_proj), :127 (LM
+ * head). a: bf16 [rows, in_features], row stride lda; weight: bf16
+ * [out_features, in_features], row stride ldw; out: bf16 [rows,
+ * out_features], row stride ldo. lda and ldw multiples of 8, a and weight
+ * 16-byte aligned; in_features a multiple of 64 (else LM_EUNSUPPORTED). Any
+ * out_features (the last column tile is masked). */
+int lm_linear(const void *a, int64_t lda, const void *weight, int64_t ldw,
+              int64_t rows, int64_t out_features, int64_t in_features,
+              void *out, int64_t ldo, void *stream);
+
 /* ------------------------------------------------------ fused decode ops -- */
 
 /* Residual add, RMSNorm and the router in one pass per token:

@@ -1,0 +1,227 @@
+// Dense projection for prefill-sized (and above-128-row decode) row counts on
+// MFMA with LDS tiles:
+//
+//   out[m, n] = bf16( sum_k a[m, k] * w[n, k] )          (fp32 accumulation)
+//
+// w is an nn.Linear weight [N, K] (row-major, row stride ldw), a is bf16
+// [M, K] with row stride lda, out is bf16 [M, N] with row stride ldo.
+//
+// Each output element is reduced by one workgroup over all of K, in k steps
+// of 32 taken in ascending order (one v_mfma_f32_16x16x32_bf16 per step and
+// 16x16 block). The order depends neither on M nor on the row's or tile's
+// position, so a row's result is the same bits in any batch, in any launch,
+// eager or replayed from a graph (no split-K partials, no atomics, no stream-K
+// fix-up whose summation order the caller cannot see).
+//
+// Workgroup = kTM x kTN output tile (256 x 256 or 128 x 128), kWM x kWN
+// waves, each wave a (kTM/kWM) x (kTN/kWN) block of 16 x 16 MFMA tiles; K
+// runs in steps of 64.
+// The next step's A and B rows are loaded into registers while the MFMAs run
+// on the current step's LDS tile, then stored into the other of two LDS
+// buffers (one barrier per step). An LDS row is 64 bf16 = 8 chunks of 16
+// bytes; chunk c of tile row r sits at position c ^ (r & 7), so the 16 rows of
+// one fragment read spread over the banks and each wave's stores fill 1 KB
+// contiguously. The weights are the MFMA's first operand, so a lane ends with
+// four consecutive output columns of one row and stores them as one 8-byte
+// word.
+//
+// Workgroups are dealt to the 8 XCDs round-robin in launch order; they are
+// remapped so each XCD takes a contiguous range of row tiles with all their
+// column tiles: a row tile's A rows are fetched into one L2 and reused there
+// by every column tile.
+//
+// Reference: the packed QKV and output projections of litemoe/model.py:47-49
+// and :60 (F.linear over the packed prefill rows), and the LM head :127.
+#include "internal.h"
+
+namespace lm {
+namespace {
+
+constexpr int kBK = 64;
+constexpr int kXcds = 8;
+constexpr int kRowBytes = kBK * 2;  // 128
+
+__device__ __forceinline__ int frag_offset(int row, int chunk) {
+  return row * kRowBytes + ((chunk ^ (row & 7)) << 4);
+}
+
+// kVec: ldo and out allow 8-byte stores and N % 4 == 0 (else 2-byte stores).
+template <int kTM, int kTN, int kWM, int kWN, bool kVec>
+__global__ void __launch_bounds__(64 * kWM * kWN)
+gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w, int64_t ldw,
+            bf16 *__restrict__ out, int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n,
+            int xcd_remap) {
+  constexpr int kWaves = kWM * kWN;
+  constexpr int kWaveRows = kTM / kWM, kWaveCols = kTN / kWN;
+  constexpr int kRB = kWaveRows / 16, kCB = kWaveCols / 16;
+  constexpr int kLA = kTM / (8 * kWaves), kLB = kTN / (8 * kWaves);  // 16-byte loads per lane
+  static_assert(kLA * 8 * kWaves == kTM && kLB * 8 * kWaves == kTN, "tile rows per load round");
+  constexpr int kABytes = kTM * kRowBytes, kStage = (kTM + kTN) * kRowBytes;
+  __shared__ __align__(16) char smem[2 * kStage];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lin = blockIdx.x;
+  int tile_m = lin / tiles_n, tile_n = lin % tiles_n;
+  if (xcd_remap) {  // grid = tiles_n * (tiles_m rounded up to a multiple of 8)
+    const int per_xcd = (int)(gridDim.x / kXcds) / tiles_n;  // row tiles per XCD
+    const int j = lin / kXcds;
+    tile_m = (lin % kXcds) * per_xcd + j / tiles_n;
+    tile_n = j % tiles_n;
+  }
+  if (tile_m >= tiles_m) return;
+  const int m0 = tile_m * kTM, n0 = tile_n * kTN;
+
+  // Load instruction i of wave w fills LDS rows 8*(w*L+i) .. +7 (1 KB):
+  // lane l writes row 8*(w*L+i) + l/8 at position l%8, holding chunk
+  // (l%8) ^ (l/8), which is frag_offset's swizzle. Rows past M or N repeat
+  // the last row (finite values; their outputs are not stored).
+  // 32-bit element offsets (the host checks that every row start fits).
+  const int chunk = (lane & 7) ^ (lane >> 3);
+  uint32_t oa[kLA], ob[kLB];
+#pragma unroll
+  for (int i = 0; i < kLA; ++i) {
+    const int r = min(m0 + 8 * (wave * kLA + i) + lane / 8, M - 1);
+    oa[i] = (uint32_t)r * (uint32_t)lda + chunk * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < kLB; ++i) {
+    const int r = min(n0 + 8 * (wave * kLB + i) + lane / 8, N - 1);
+    ob[i] = (uint32_t)r * (uint32_t)ldw + chunk * 8;
+  }
+  u32x4 ra[kLA], rb[kLB];
+  auto load = [&](int kt) {
+    const uint32_t k0 = kt * kBK;
+#pragma unroll
+    for (int i = 0; i < kLA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a + (oa[i] + k0));
+#pragma unroll
+    for (int i = 0; i < kLB; ++i) rb[i] = *reinterpret_cast<const u32x4 *>(w + (ob[i] + k0));
+  };
+  auto store = [&](int buf) {
+    char *base = smem + buf * kStage + lane * 16;
+#pragma unroll
+    for (int i = 0; i < kLA; ++i) *reinterpret_cast<u32x4 *>(base + (wave * kLA + i) * 1024) = ra[i];
+#pragma unroll
+    for (int i = 0; i < kLB; ++i)
+      *reinterpret_cast<u32x4 *>(base + kABytes + (wave * kLB + i) * 1024) = rb[i];
+  };
+
+  const int wr = wave / kWN, wc = wave % kWN;
+  const int fr = lane % 16, fk = lane / 16;
+  f32x4 acc[kRB][kCB];
+#pragma unroll
+  for (int i = 0; i < kRB; ++i)
+#pragma unroll
+    for (int jj = 0; jj < kCB; ++jj) acc[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf) {
+    const char *as = smem + buf * kStage;
+    const char *bs = as + kABytes;
+#pragma unroll
+    for (int kk = 0; kk < kBK / 32; ++kk) {
+      u32x4 bfr[kCB];
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb)
+        bfr[cb] = *reinterpret_cast<const u32x4 *>(bs + frag_offset(wc * kWaveCols + cb * 16 + fr, kk * 4 + fk));
+#pragma unroll
+      for (int rb2 = 0; rb2 < kRB; ++rb2) {
+        const u32x4 af = *reinterpret_cast<const u32x4 *>(
+            as + frag_offset(wr * kWaveRows + rb2 * 16 + fr, kk * 4 + fk));
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb) acc[rb2][cb] = mfma16x16x32(bfr[cb], af, acc[rb2][cb]);
+      }
+    }
+  };
+
+  const int nk = K / kBK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) load(kt + 1);
+    __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
+    compute(kt & 1);
+    // The other buffer was last read in step kt - 1, which every wave has
+    // left (the barrier below closed it).
+    if (more) store((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  // Transposed C fragment: lane holds output row m0 + wr*kWaveRows + rb*16 +
+  // lane%16 and its columns 4*(lane/16) .. +3 of each 16-column block.
+#pragma unroll
+  for (int rb2 = 0; rb2 < kRB; ++rb2) {
+    const int row = m0 + wr * kWaveRows + rb2 * 16 + fr;
+    if (row >= M) continue;
+    bf16 *o = out + (int64_t)row * ldo;
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb) {
+      const int col = n0 + wc * kWaveCols + cb * 16 + 4 * fk;
+      const f32x4 v = acc[rb2][cb];
+      if constexpr (kVec) {
+        if (col < N)
+          *reinterpret_cast<uint2 *>(o + col) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (col + i < N) o[col + i] = (bf16)f32_to_bf16(v[i]);
+      }
+    }
+  }
+}
+
+template <int TM, int TN, int WM, int WN>
+int launch_gemm_cfg(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16 *out, int64_t ldo,
+                    int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  const int64_t tiles_m = cdiv(M, TM), tiles_n = cdiv(N, TN);
+  // With fewer row tiles than XCDs the remap would put every tile on a few
+  // XCDs; the plain order spreads the column tiles instead.
+  const bool remap = tiles_m >= kXcds;
+  const int64_t blocks = (remap ? align_up(tiles_m, kXcds) : tiles_m) * tiles_n;
+  const bool vec = N % 4 == 0 && ldo % 4 == 0 && ((uintptr_t)out & 7) == 0;
+  if (vec)
+    gemm_kernel<TM, TN, WM, WN, true><<<dim3((unsigned)blocks), 64 * WM * WN, 0, stream>>>(
+        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap);
+  else
+    gemm_kernel<TM, TN, WM, WN, false><<<dim3((unsigned)blocks), 64 * WM * WN, 0, stream>>>(
+        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap);
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+}  // namespace
+
+bool gemm_shape_ok(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
+  const int64_t tiles = align_up(cdiv(M, 128), kXcds) * cdiv(N, 128);
+  const int64_t lim = (int64_t)1 << 31;
+  return M > 0 && N > 0 && K > 0 && K % kBK == 0 && (M - 1) * lda + K < lim &&
+         (N - 1) * ldw + K < lim && tiles < lim;
+}
+
+// Prefill-sized row counts take 256 x 256 tiles (eight waves of 64 x 128:
+// half the LDS reads per MFMA of 64 x 64 wave tiles); measured at the cfg 4
+// QKV shape (46,990 x 1536 x 2560) 426 us against 582 us for 128 x 128 tiles
+// (two workgroups per CU) and 494-635 us for 128 x 256 / 256 x 128. Fewer rows
+// keep 128 x 128 tiles, whose grid spreads over more CUs.
+int launch_gemm(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16 *out, int64_t ldo,
+                int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  if (M >= 2048)
+    return launch_gemm_cfg<256, 256, 4, 2>(a, lda, w, ldw, out, ldo, M, N, K, stream);
+  return launch_gemm_cfg<128, 128, 2, 2>(a, lda, w, ldw, out, ldo, M, N, K, stream);
+}
+
+}  // namespace lm
+
+using namespace lm;
+
+extern "C" int lm_linear(const void *a, int64_t lda, const void *weight, int64_t ldw, int64_t rows,
+                         int64_t out_features, int64_t in_features, void *out, int64_t ldo,
+                         void *stream) {
+  LM_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0 && lda >= in_features &&
+             ldw >= in_features && ldo >= out_features && lda % 8 == 0 && ldw % 8 == 0);
+  if (rows == 0) return LM_OK;
+  if (!gemm_shape_ok(rows, out_features, in_features, lda, ldw)) return LM_EUNSUPPORTED;
+  LM_REQUIRE(a && weight && out);
+  LM_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)weight & 15) == 0 && ((uintptr_t)out & 1) == 0);
+  return launch_gemm((const bf16 *)a, lda, (const bf16 *)weight, ldw, (bf16 *)out, ldo, rows,
+                     out_features, in_features, (hipStream_t)stream);
+}

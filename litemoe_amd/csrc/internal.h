@@ -71,3 +71,13 @@ int launch_expert_gemm_down(const bf16 *act, const bf16 *w2, const int32_t *offs
                             hipStream_t stream);
 
 }  // namespace lm
+
+namespace lm {
+
+// gemm.hip: dense out = bf16(a . w^T), one workgroup per 128 x 128 output tile
+// reducing all of K in ascending order.
+bool gemm_shape_ok(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw);
+int launch_gemm(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16 *out, int64_t ldo,
+                int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+}  // namespace lm

@@ -17,8 +17,11 @@ The engine runs one GPU (world 1). What differs is how a step runs:
 * when to stop is read from the delivered snapshots (a row ends when its
   outputs reach its budget or its last token is a stop id), so the loop
   polls without a device synchronisation;
-* prefill is packed and ragged (litemoe/packed.py:19-36), in chunks of at
-  most ``prefill_tokens`` tokens.
+* ``prefill`` runs one ``forward(..., slot=j)`` per request as the
+  reference's plain engine does (engine.py:128-148); the model executes each
+  on its packed kernels. The batched engines (``batch.BatchPrefillEngine``,
+  ``optimized.OptimizedEngine``) prefill every request in one padded or
+  packed call instead.
 """
 import math
 import time
@@ -28,7 +31,6 @@ import torch
 
 from .cache import KVCache
 from .execution import OutputRing, capture_decode
-from .packed import packed_prefill_logits
 from .step import greedy_epilogue
 
 CONTEXT_LIMIT = 4096
@@ -69,7 +71,7 @@ def plan_requests(requests, cfg, mode, capacity, rope_rows):
     need = max((len(r.prompt) + r.budget - 1 for r in live), default=1)
     if need > limit:
         raise ValueError("Request exceeds the model context limit")
-    if capacity is None:
+    if not capacity:  # None or 0 chooses, as the reference's `capacity or ...` (engine.py:47)
         capacity = need if mode == "eager" else 1 << math.ceil(math.log2(need))
     if not need <= capacity <= limit:
         raise ValueError("Insufficient/unsupported KV capacity")
@@ -80,7 +82,6 @@ def plan_requests(requests, cfg, mode, capacity, rope_rows):
 
 class Engine:
     cache_type = KVCache
-    prefill_tokens = 1 << 17
     ring_depth = 4
 
     def __init__(self, model, requests, world=1, rank=0, mode="eager", ignore_eos=False, poll=1,
@@ -96,6 +97,9 @@ class Engine:
         self.requests, self.empty, self.capacity = plan.live, plan.empty, plan.capacity
         self.local = self.requests
         self.batch = len(self.requests)
+        # prefill rounds: the longest prompt of each group of `world` requests
+        # (litemoe/engine.py:69); with one rank, each request's prompt length
+        self.rounds = [len(r.prompt) for r in self.requests]
         self.mode, self.ignore_eos, self.poll, self.host_process = mode, ignore_eos, poll, host_process
         self.graph = None
         self.ring = None
@@ -173,25 +177,11 @@ class Engine:
         torch.cuda.synchronize(self.device)
 
     # -- prefill -------------------------------------------------------------------
-    def prefill_logits(self, prompts):
-        """Last-position logits of every prompt, packed in token-bounded chunks."""
-        chunks, start = [], 0
-        while start < len(prompts):
-            end, tokens = start + 1, len(prompts[start])
-            while end < len(prompts) and tokens + len(prompts[end]) <= self.prefill_tokens:
-                tokens += len(prompts[end])
-                end += 1
-            self.model.ep.capacity = max(self.model.ep.capacity, tokens)
-            self.model.ep.prepare(tokens)
-            chunks.append(packed_prefill_logits(self.model, prompts[start:end], self.cache, start))
-            start = end
-        return chunks[0] if len(chunks) == 1 else torch.cat(chunks)
-
-    def prefill(self):
-        """Prefill every request and set the state for the first decode step:
-        the first token, lengths, one output generated, and the row active
-        unless its budget is 1 or (without ignore_eos) the token stops it."""
-        first = self.prefill_logits([r.prompt for r in self.local])[:, 0].argmax(-1)
+    def start_rows(self, first):
+        """State for the first decode step after a prefill that chose the
+        tokens ``first``: lengths, one output generated, and each row active
+        unless its budget is 1 or (without ignore_eos) the token stops it
+        (litemoe/batch.py:57-64)."""
         s = self.state
         s["next"].copy_(first)
         s["length"].copy_(torch.tensor([len(r.prompt) for r in self.local], device=self.device))
@@ -200,6 +190,20 @@ class Engine:
         if not self.ignore_eos:
             keep &= ~self.is_eos(first)
         s["active"].copy_(keep)
+
+    def prefill(self):
+        """One forward per request into its own cache row, as
+        litemoe/engine.py:128-148 (``slot=j``, the last prompt position)."""
+        firsts = []
+        for j, length in enumerate(self.rounds):
+            prompt = self.local[j].prompt
+            tokens = torch.tensor([prompt], device=self.device)
+            pos = torch.arange(len(prompt), device=self.device)[None, :]
+            valid = torch.ones_like(tokens, dtype=torch.bool)
+            logits = self.model.forward(tokens, pos, valid, self.cache, slot=j, last=len(prompt) - 1,
+                                        communication_tokens=length)
+            firsts.append(logits[0, 0].argmax(-1))
+        self.start_rows(torch.stack(firsts))
 
     # -- generation ------------------------------------------------------------------
     def _consume(self, rows):
@@ -243,8 +247,13 @@ class Engine:
         self.ring.start()
         steps = max(self.budgets) - 1
         for n in range(steps):
-            if not self.ignore_eos and n % self.poll == 0 and not open_rows:
-                break
+            if not self.ignore_eos and n % self.poll == 0:
+                # Snapshots arrive up to ring_depth - 1 steps late in the
+                # asynchronous mode; no replay is queued once every row is
+                # known closed, or once no open row has budget left for it
+                # (step n emits each row's output n + 2).
+                if not open_rows or n + 2 > max(self.budgets[j] for j in open_rows):
+                    break
             if step_events is not None:
                 begin, finish = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 begin.record()

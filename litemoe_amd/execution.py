@@ -31,6 +31,23 @@ import torch
 from . import _lib
 
 
+# Pinned host buffers and events of output rings that were dropped while a
+# stream capture was running: freeing them then makes runtime calls that a
+# capture forbids (the process aborts), so they are kept here and released
+# at the next point known to be outside a capture.
+_PARKED = []
+
+
+def _capturing():
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
+def release_parked():
+    """Free the ring buffers parked during a capture (no-op inside one)."""
+    if _PARKED and not _capturing():
+        _PARKED.clear()
+
+
 class StepGraph:
     """One recorded decode step; :meth:`replay` launches it on the current stream."""
 
@@ -85,6 +102,7 @@ def capture_decode(step, reset, warmups=2, pool=None):
     caller.wait_stream(stream)
     reset()
     torch.cuda.synchronize(caller.device)
+    release_parked()
     return StepGraph(graph, stream, graph.pool() if pool is None else pool)
 
 
@@ -102,8 +120,16 @@ class OutputRing:
         self._device_ptr = None
         self.counter = None
         if asynchronous:
+            release_parked()
             self.host = torch.empty((depth, *emit.shape), dtype=emit.dtype, pin_memory=True)
             self.events = [torch.cuda.Event() for _ in range(depth)]
+
+    def __del__(self):
+        # Dropped during a capture (e.g. a finished engine collected while a
+        # caller records its own graph): keep the pinned slots and events
+        # alive until release_parked() runs outside the capture.
+        if getattr(self, "asynchronous", False) and hasattr(self, "host") and _capturing():
+            _PARKED.append((self.host, self.events))
 
     # -- device view -----------------------------------------------------
     def device_target(self, rows):

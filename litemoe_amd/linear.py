@@ -129,3 +129,33 @@ def linear(a, weight, splits=None):
     if splits is None:
         raise ValueError(f"No split-K kernel for rows={a.shape[0]}, weight {tuple(weight.shape)}")
     return reduce(linear_splitk(a, weight, splits))
+
+
+def linear_dense(a, weight, out=None):
+    """``F.linear(a, weight)`` (bf16, no bias) for any row count on
+    ``lm_linear``: one workgroup reduces each output over all of K in
+    ascending order, so a row's bits do not depend on the batch or the
+    launch. ``a [rows, K]`` with contiguous rows (any row stride),
+    ``weight [N, K]`` with contiguous rows; ``out [rows, N]`` (optional, any
+    row stride) receives the result."""
+    _lib.require_cuda(a, weight, what="projection operands")
+    if a.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("Dense projection supports BF16 operands")
+    if a.dim() != 2 or weight.dim() != 2 or a.shape[1] != weight.shape[1]:
+        raise ValueError("Dense projection needs a [rows, K] input and an [N, K] weight")
+    rows, k = a.shape
+    n = weight.shape[0]
+    if k % 64:
+        raise ValueError("Dense projection needs in_features a multiple of 64")
+    if rows and (a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16):
+        raise ValueError("Dense projection needs 16-byte aligned input rows with a stride a multiple of 8")
+    if weight.stride(1) != 1 or weight.stride(0) % 8 or weight.data_ptr() % 16:
+        raise ValueError("Dense projection needs 16-byte aligned weight rows with a stride a multiple of 8")
+    if out is None:
+        out = torch.empty(rows, n, device=a.device, dtype=torch.bfloat16)
+    elif out.shape != (rows, n) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError("Output must be bf16 [rows, out_features] with unit column stride")
+    if rows:
+        _lib.call("lm_linear", a.data_ptr(), max(a.stride(0), k), weight.data_ptr(), max(weight.stride(0), k),
+                  rows, n, k, out.data_ptr(), max(out.stride(0), n), _lib.stream(a.device))
+    return out

@@ -5,10 +5,10 @@ slot=None, last=None, communication_tokens=None)`` keeps the reference's
 signature and tensor layouts. Per layer (decode and packed prefill alike):
 
     x += r * y_prev; z = rmsnorm(x)          lm_add_rmsnorm (layer 0: plain norm)
-    qkv = z . Wqkv^T                         hipBLASLt (packed q|k|v, model.py:37-40,47-49)
+    qkv = z . Wqkv^T                         lm_linear (packed q|k|v, model.py:37-40,47-49)
     rope(q, k); k, v -> cache                lm_rope_kv_write
     a = attention(q, cache or packed k/v)    lm_flash_decode | lm_prefill_attention
-    a = a . Wo^T                             hipBLASLt
+    a = a . Wo^T                             lm_linear
     x += r * a; z = rmsnorm(x)               lm_add_rmsnorm
     w, ids = router(z)                       lm_router (GEMV + top-k + softmax)
     y = experts(z, ids, w)                   lm_fused_experts (align, gate_up, down, finish)
@@ -22,8 +22,10 @@ next layer's norm). In lean decode (rows <= 128) the dense projections are
 split-K MFMA kernels (``lm_linear_splitk``) whose fp32 partials are summed
 by their consumers: ``lm_flash_decode_qkv`` (QKV reduction, RoPE, KV store
 and attention in one launch) and ``lm_add_rmsnorm_router_splitk``; a decode
-layer is then seven hand-written launches. Prefill projections use the
-vendor BLAS (F.linear). There is no CPU path.
+layer is then seven hand-written launches. Every other projection (packed
+prefill, decode above 128 rows, the LM head of ``forward``) is ``lm_linear``,
+which reduces each output over K in one fixed order: no vendor BLAS runs on
+the path, and a row's bits do not depend on the batch. There is no CPU path.
 """
 import torch
 import torch.nn.functional as F
@@ -32,9 +34,9 @@ from . import _lib
 from .config import validate_config
 from .flash_decode import FlashDecode
 from .experts import finish_add_rmsnorm, pack_expert_weights, scan_path
-from .linear import linear_splitk, linear_splitk_frag, pick_splits
+from .linear import linear_dense, linear_splitk, linear_splitk_frag, pick_splits
 from .norm import add_rmsnorm
-from .packed import PackedPrefill, varlen_attention
+from .packed import PackedPrefill, build_packed, varlen_attention
 from .rope import rope_kv_write
 from .router import add_rmsnorm_route as route_add_rmsnorm
 from .router import add_rmsnorm_route_splitk as route_add_rmsnorm_splitk
@@ -43,12 +45,23 @@ from .step import PackedHead, decode_prologue, greedy_epilogue, greedy_head, hea
 
 
 class Granite:
-    def __init__(self, cfg, weights, ep, capacity):
+    """The reference's ``Granite(cfg, weights, ep, capacity)``.
+
+    ``pack_weights`` (default True) makes the decode copies of the expert
+    weights and the LM head in MFMA fragment order once at construction
+    (``lm_expert_pack``, ``lm_head_pack``): about 6 GB for the 32-layer 3B
+    model plus 151 MB for its head. With False no copy is made; decode then
+    reads the checkpoint layout (the same scan kernels on row-major weights)
+    and takes the LM head through ``lm_linear`` and the greedy epilogue."""
+
+    def __init__(self, cfg, weights, ep, capacity, pack_weights=True):
         validate_config(cfg)
+        self.pack_weights = bool(pack_weights)
         self.cfg, self.w, self.ep = cfg, weights, ep
         self.trace = None
         self.decode_flash = None   # FlashDecode set by the execution policy
         self.decode_lean = False   # positions pre-zeroed for stopped rows; outputs unmasked
+        self.prefill_lean = False  # set by the optimized policy: batched prefill is packed
         self.used = None
         self._row_order = None     # the decode prologue's row order, during greedy_step only
         self.fused_head = True     # greedy_step: LM head with the argmax in its epilogue (lm_head_greedy)
@@ -63,12 +76,14 @@ class Granite:
         self.cos_sin = torch.cat((freq.cos(), freq.sin()), -1).to(dtype)
         self.cos, self.sin = [half.repeat(1, 2) for half in self.cos_sin.chunk(2, -1)]
         self.prepare_packed_qkv()
-        self.prepare_packed_experts()
-        # The head in the fused greedy head's fragment order (a second copy,
-        # made once; the embedding keeps the checkpoint layout).
-        head = weights["head"]
-        self.packed_head = (PackedHead(head) if head.is_cuda and head.is_contiguous() and
-                            head_supported(1, head.shape[0], cfg.hidden_size) else None)
+        self.packed_head = None
+        if self.pack_weights:
+            self.prepare_packed_experts()
+            # The head in the fused greedy head's fragment order (a second
+            # copy, made once; the embedding keeps the checkpoint layout).
+            head = weights["head"]
+            self.packed_head = (PackedHead(head) if head.is_cuda and head.is_contiguous() and
+                                head_supported(1, head.shape[0], cfg.hidden_size) else None)
 
     def prepare_packed_qkv(self):
         for w in self.w["layers"]:
@@ -108,7 +123,7 @@ class Granite:
         rows = z.shape[0]
         d = cfg.hidden_size // cfg.num_attention_heads
         hq, hkv = cfg.num_attention_heads, cfg.num_key_value_heads
-        qkv = F.linear(z, w["self_attn.qkv_proj"])
+        qkv = linear_dense(z, w["self_attn.qkv_proj"])
         q = qkv[:, :hq * d].view(rows, hq, d)
         k = qkv[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
         v = qkv[:, (hq + hkv) * d:].view(rows, hkv, d)
@@ -121,11 +136,11 @@ class Granite:
             flash = self._decode_attention(rows, cache)
             a = flash(q.unsqueeze(2), cache.k[layer], cache.v[layer], positions, active,
                       cfg.attention_multiplier, self.used)
-        return F.linear(a.reshape(rows, hq * d), w["self_attn.o_proj"])
+        return linear_dense(a.reshape(rows, hq * d), w["self_attn.o_proj"])
 
     def decode_splits(self, rows):
         """K-slice counts (qkv, o_proj) of the split-K decode projections, or
-        None when a shape has no kernel (the layer then uses F.linear)."""
+        None when a shape has no kernel (the layer then uses lm_linear)."""
         cfg = self.cfg
         d = cfg.hidden_size // cfg.num_attention_heads
         # lm_add_rmsnorm_router_splitk: hidden 512*{1..4}, at most 4 slices
@@ -180,7 +195,7 @@ class Granite:
                 a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
                 weights, ids, z = route_add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps,
                                                     w["block_sparse_moe.router.layer"], k, z)
-            if "input_linear_packed" in w and scan_path(x.shape[0], k):
+            if self.pack_weights and "input_linear_packed" in w and scan_path(x.shape[0], k):
                 # decode: the fragment layout (1 KB per weight-fragment load)
                 y = self.ep.backend.routes(z, w["input_linear_packed"], w["output_linear_packed"], ids,
                                            packed=True)
@@ -228,17 +243,28 @@ class Granite:
             greedy_head(z, self.packed_head, cfg.logits_scaling, valid, state, emit, eos, ignore_eos,
                         ring_target=target)
         else:
-            greedy_epilogue(F.linear(z, head), cfg.logits_scaling, valid, state, emit, eos,
+            greedy_epilogue(linear_dense(z, head), cfg.logits_scaling, valid, state, emit, eos,
                             ignore_eos, ring_target=target)
 
     def forward(self, tokens, positions, valid, cache, slot=None, last=None, communication_tokens=None):
+        """Logits ``[rows, positions, V] / logits_scaling`` (litemoe/model.py:95-127).
+
+        ``slot=None``: one decode step, ``tokens [B, 1]``. ``slot`` a
+        :class:`PackedPrefill`: the packed ragged prefill, one row of all
+        prompts. ``slot`` an int or a slice: a right-padded prefill of
+        ``tokens [b, s]`` into cache rows ``slot`` (``valid`` a prefix of each
+        row, ``positions`` the column index), run on the packed kernels
+        (:meth:`_padded_prefill`). ``last`` keeps one position per row (an
+        int, or a tensor of per-row positions; for a packed row, flat token
+        indices). ``communication_tokens`` sizes the reference's EP2
+        exchange and is not used on one GPU."""
+        if slot is not None and not isinstance(slot, PackedPrefill):
+            return self._padded_prefill(tokens, positions, valid, cache, slot, last)
         cfg = self.cfg
         packed = isinstance(slot, PackedPrefill)
-        if slot is not None and not packed:
-            raise ValueError("Prefill on this path is packed (use packed_prefill_logits)")
         _lib.require_cuda(tokens, positions, valid, cache.k, what="model inputs")
         b, s = tokens.shape
-        hidden, eps, r = cfg.hidden_size, cfg.rms_norm_eps, cfg.residual_multiplier
+        hidden = cfg.hidden_size
         valid_rows = valid.reshape(-1)
         if packed:
             rope_positions, flat_positions = slot.positions, slot.positions
@@ -252,30 +278,9 @@ class Granite:
             # seqused_k of flash_decode.py:21 / model.py:103
             self.used = ((rope_positions + 1) if lean else
                          torch.where(valid_rows, flat_positions + 1, 1)).to(torch.int32)
-        masked = not packed and not self.decode_lean
         x = (F.embedding(tokens, self.w["embedding"]) * cfg.embedding_multiplier).reshape(b * s, hidden)
         x = x.contiguous()
-        layers = self.w["layers"]
-        z = add_rmsnorm(x, None, r, layers[0]["input_layernorm"], eps)
-        if not masked and self._fused_moe():
-            z = self._fused_layers(x, z, cache, rope_positions, valid_rows, flat_positions, slot)
-        else:
-            y = None
-            for layer, w in enumerate(layers):
-                if layer:
-                    add_rmsnorm(x, y, r, w["input_layernorm"], eps, out=z)
-                a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
-                if masked:
-                    a = a * valid_rows[:, None]
-                add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps, out=z)
-                scales, ids = route(z, w["block_sparse_moe.router.layer"], cfg.num_experts_per_tok)
-                if packed or not self.decode_lean:
-                    # outside the fused paths the reference hands the experts
-                    # bf16 scales (litemoe/model.py:117-118)
-                    scales = scales.to(torch.bfloat16)
-                y = self.ep(z, ids, scales, valid_rows, w["physical"], w["input_linear"], w["output_linear"],
-                            w["logical"], decode=True, tokens=communication_tokens)
-            z = add_rmsnorm(x, y, r, self.w["norm"], eps, out=z)
+        z = self._layers(x, cache, rope_positions, valid_rows, flat_positions, slot, communication_tokens)
         if last is not None:
             # row i keeps position last[i] (litemoe/model.py:123-125); a packed
             # batch is one row, so its `last` are flat token indices
@@ -284,4 +289,93 @@ class Granite:
             out_rows = (z.shape[0], 1)
         else:
             out_rows = (b, s)
-        return (F.linear(z, self.w["head"]) / cfg.logits_scaling).view(*out_rows, -1)
+        return (linear_dense(z, self.w["head"]) / cfg.logits_scaling).view(*out_rows, -1)
+
+    def _layers(self, x, cache, rope_positions, valid_rows, flat_positions, slot, communication_tokens=None):
+        """The layer stack over the rows of ``x [rows, H]`` (the residual
+        stream, updated in place); returns the final norm's output."""
+        cfg = self.cfg
+        eps, r = cfg.rms_norm_eps, cfg.residual_multiplier
+        packed = isinstance(slot, PackedPrefill)
+        masked = not packed and not self.decode_lean
+        layers = self.w["layers"]
+        z = add_rmsnorm(x, None, r, layers[0]["input_layernorm"], eps)
+        if not masked and self._fused_moe():
+            return self._fused_layers(x, z, cache, rope_positions, valid_rows, flat_positions, slot)
+        y = None
+        for layer, w in enumerate(layers):
+            if layer:
+                add_rmsnorm(x, y, r, w["input_layernorm"], eps, out=z)
+            a = self.attention(z, w, cache, layer, rope_positions, valid_rows, flat_positions, slot)
+            if masked:
+                a = a * valid_rows[:, None]
+            add_rmsnorm(x, a, r, w["post_attention_layernorm"], eps, out=z)
+            scales, ids = route(z, w["block_sparse_moe.router.layer"], cfg.num_experts_per_tok)
+            if packed or not self.decode_lean:
+                # outside the fused paths the reference hands the experts
+                # bf16 scales (litemoe/model.py:117-118)
+                scales = scales.to(torch.bfloat16)
+            y = self.ep(z, ids, scales, valid_rows, w["physical"], w["input_linear"], w["output_linear"],
+                        w["logical"], decode=True, tokens=communication_tokens)
+        return add_rmsnorm(x, y, r, self.w["norm"], eps, out=z)
+
+    def _padded_prefill(self, tokens, positions, valid, cache, slot, last):
+        """Right-padded prefill into cache rows ``slot`` (an int: one row; a
+        slice: ``b`` rows), litemoe/model.py:95-127 with ``slot`` not None.
+
+        The reference runs every position through SDPA with a padding mask
+        and stores ``k * valid`` in cache positions ``0 .. s-1``
+        (litemoe/cache.py:21-33). Here each row's valid prefix becomes one
+        sequence of a packed batch (the same kernels as the packed prefill,
+        so padding costs no work), and its KV lands in the row's cache
+        positions ``0 .. n-1``; positions ``n .. s-1`` are zeroed. A padding
+        position's residual stream keeps its scaled embedding, as in the
+        reference, where its attention output is masked to zero and its
+        expert rows enter as zeros: its logits (``last`` may point there)
+        are those of ``norm(embedding * multiplier)``."""
+        cfg = self.cfg
+        _lib.require_cuda(tokens, positions, valid, cache.k, what="model inputs")
+        b, s = tokens.shape
+        if isinstance(slot, slice):
+            rows = list(range(*slot.indices(cache.k.shape[1])))
+        else:
+            rows = [int(slot)]
+        if len(rows) != b or not all(0 <= row < cache.k.shape[1] for row in rows):
+            raise ValueError("Prefill slots must name one cache row per batch row")
+        if tuple(positions.shape) != (b, s) or tuple(valid.shape) != (b, s):
+            raise ValueError("tokens, positions and valid must all be [rows, width]")
+        device = tokens.device
+        valid = valid.to(torch.bool)
+        columns = torch.arange(s, device=device)
+        counts = valid.sum(1)
+        right_padded = (valid == (columns[None] < counts[:, None])).all()
+        in_order = ((positions == columns[None]) | ~valid).all()
+        host = torch.cat((counts, torch.stack((right_padded, in_order)).long())).tolist()
+        counts, ok = host[:b], all(host[b:])
+        if not ok:
+            raise ValueError("Padded prefill needs right-padded rows: valid a prefix of each row "
+                             "and positions equal to the column index")
+        if s > cache.capacity:
+            raise ValueError("Prompt width exceeds the KV capacity")
+        for row, n in zip(rows, counts):  # cache.py:28-29 stores k * valid: zeros past the prompt
+            if n < s:
+                cache.k[:, row, :, n:s].zero_()
+                cache.v[:, row, :, n:s].zero_()
+        x = (F.embedding(tokens, self.w["embedding"]) * cfg.embedding_multiplier).reshape(b * s, cfg.hidden_size)
+        x = x.contiguous()
+        live = [i for i, n in enumerate(counts) if n]
+        if live:
+            packed, _ = build_packed([counts[i] for i in live], device, slots=[rows[i] for i in live])
+            index = valid.reshape(-1).nonzero().flatten()  # row-major: each row's prefix in order
+            xv = x.index_select(0, index)
+            self._layers(xv, cache, packed.positions, torch.ones(xv.shape[0], dtype=torch.bool, device=device),
+                         packed.positions, packed)
+            x.index_copy_(0, index, xv)
+        if last is not None:
+            last = last.long().to(device) if isinstance(last, torch.Tensor) else torch.tensor(last, device=device)
+            x = x[torch.arange(b, device=device) * s + last]
+            out_rows = (b, 1)
+        else:
+            out_rows = (b, s)
+        z = add_rmsnorm(x.contiguous(), None, cfg.residual_multiplier, self.w["norm"], cfg.rms_norm_eps)
+        return (linear_dense(z, self.w["head"]) / cfg.logits_scaling).view(*out_rows, -1)

@@ -15,15 +15,19 @@ The policy chooses:
   which lets the layer tail run fused (``Granite.greedy_step``). It needs
   this library's experts (the ``native`` capability) and the identity
   expert placement, as the reference's lean mode needs vLLM's experts and
-  the identity placement (optimized.py:32-33).
+  the identity placement (optimized.py:32-33);
+* ``prefill_lean`` -- lean and the engine's ``lean_prefill``: the batched
+  prefill packs every prompt into one ragged batch
+  (``packed.optimized_prefill_logits``, optimized.py:46).
 """
 from contextlib import contextmanager
 from dataclasses import dataclass
 
-from .engine import Engine
+from .batch import BatchPrefillEngine
 from .flash_decode import FlashDecode
+from .packed import optimized_prefill_logits
 
-_MODEL_FLAGS = ("decode_flash", "decode_lean")
+_MODEL_FLAGS = ("decode_flash", "decode_lean", "prefill_lean")
 
 
 @dataclass(frozen=True)
@@ -51,7 +55,8 @@ class DecodePolicy:
 
     def settings(self, run):
         """Model attribute values under this policy."""
-        return {"decode_flash": run.flash_attention if self.flash else None, "decode_lean": self.lean}
+        return {"decode_flash": run.flash_attention if self.flash else None, "decode_lean": self.lean,
+                "prefill_lean": self.lean and bool(getattr(run, "lean_prefill", True))}
 
 
 @contextmanager
@@ -80,9 +85,11 @@ def optimized_policy(run):
         model.ep.decode_lean = saved_ep
 
 
-class OptimizedEngine(Engine):
+class OptimizedEngine(BatchPrefillEngine):
     flash_decode = True
     lean_decode = True
+    lean_prefill = True
+    prefill_function = staticmethod(optimized_prefill_logits)
 
     def __init__(self, *args, num_splits=None, **kwargs):
         super().__init__(*args, **kwargs)

@@ -40,17 +40,20 @@ def varlen_attention(q, k, v, cu, maximum, scale, causal=True, out=None):
     return out
 
 
-def build_packed(lengths, device, slot_start=0):
+def build_packed(lengths, device, slot_start=0, slots=None):
     """cu_seqlens, per-token positions and slots for prompts of ``lengths``
-    (packed.py:25-33)."""
+    (packed.py:25-33); sequence i goes to cache row ``slot_start + i``, or to
+    ``slots[i]`` when a list of rows is given."""
     if not lengths or min(lengths) < 1:
         raise ValueError("Packed Prefill requires nonempty prompts")
+    rows = [slot_start + i for i in range(len(lengths))] if slots is None else list(slots)
+    if len(rows) != len(lengths):
+        raise ValueError("Packed Prefill needs one cache row per prompt")
     ends = torch.tensor(lengths, dtype=torch.int32).cumsum(0, dtype=torch.int32)
     cu = torch.cat((ends.new_zeros(1), ends)).to(device)
     positions = torch.cat([torch.arange(n) for n in lengths]).to(device)
-    slots = torch.cat([torch.full((n,), slot_start + i, dtype=torch.int64)
-                       for i, n in enumerate(lengths)]).to(device)
-    return PackedPrefill(cu, max(lengths), slots, positions), ends.to(device)
+    slot_ids = torch.cat([torch.full((n,), row, dtype=torch.int64) for row, n in zip(rows, lengths)]).to(device)
+    return PackedPrefill(cu, max(lengths), slot_ids, positions), ends.to(device)
 
 
 def packed_prefill_logits(model, prompts, cache, slot_start=0):
@@ -63,3 +66,32 @@ def packed_prefill_logits(model, prompts, cache, slot_start=0):
     tokens = torch.tensor([t for p in prompts for t in p], device=cache.k.device)[None]
     return model.forward(tokens, packed.positions[None], torch.ones_like(tokens, dtype=torch.bool),
                          cache, slot=packed, last=ends.long() - 1)
+
+
+def optimized_prefill_logits(model, prompts, cache, slot_start=0, max_tokens=1 << 17):
+    """The prefill choice of litemoe/packed.py:39-51: packed when the model
+    runs the lean prefill (or, for a batch, when the longest prompt is
+    >= 1024 tokens or padding would add half again at >= 512), else one
+    right-padded batch (:func:`litemoe_amd.batch.prefill_logits`). A packed
+    prefill runs in chunks of at most ``max_tokens`` tokens (the expert
+    workspace grows with the token count). Returns ``[len(prompts), 1, V]``."""
+    from .batch import prefill_logits, prepare_batch
+    if not cache.k.is_cuda:
+        raise ValueError("Prefill runs on the GPU path only")
+    lengths = [len(p) for p in prompts]
+    width, batch = max(lengths), len(lengths)
+    lean = getattr(model, "prefill_lean", False) and min(lengths) > 0
+    if lean or (batch > 1 and min(lengths) > 0 and
+                (width >= 1024 or (width >= 512 and 3 * sum(lengths) <= 2 * batch * width))):
+        chunks, start = [], 0
+        while start < batch:
+            end, tokens = start + 1, lengths[start]
+            while end < batch and tokens + lengths[end] <= max_tokens:
+                tokens += lengths[end]
+                end += 1
+            prepare_batch(model, tokens)
+            chunks.append(packed_prefill_logits(model, prompts[start:end], cache, slot_start + start))
+            start = end
+        return chunks[0] if len(chunks) == 1 else torch.cat(chunks)
+    prepare_batch(model, batch * width)
+    return prefill_logits(model, prompts, cache, slot_start)

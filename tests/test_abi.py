@@ -45,6 +45,11 @@ def test_workspace_queries():
     assert _lib.size_query("lm_head_greedy_workspace_size", 128, 49155, 1536) == 128 * 385 * 8
 
 
+# Non-null dummy pointers: every case returns before any launch, so nothing
+# is dereferenced (the checks run on the host only).
+_P = 16
+
+
 @pytest.mark.parametrize("call,expected", [
     (lambda h: h.lm_rmsnorm(None, None, None, -1, 16, C.c_float(1e-6), None), 1),
     (lambda h: h.lm_flash_decode(None, 0, 0, None, None, None, 1, 4, 2, 8, 128, C.c_float(1.0), 8, 1, None, None,
@@ -58,14 +63,15 @@ def test_workspace_queries():
     (lambda h: h.lm_linear_splitk_frag(None, None, 4, 512, 1000, 2, None, None), 1),
     (lambda h: h.lm_flash_decode_qkv_frag(None, 3, None, 16, None, None, None, None, None, None, 200, 24, 8,
                                           1024, 64, C.c_float(1.0), 1024, 1, None, None, 0, None), 2),
+    # dense projection: K not a multiple of 64, strides below K, misaligned operands, null pointers
+    (lambda h: h.lm_linear(_P, 96, _P, 96, 4, 32, 96, _P, 32, None), 2),
+    (lambda h: h.lm_linear(_P, 64, _P, 128, 4, 32, 128, _P, 32, None), 1),
+    (lambda h: h.lm_linear(_P + 2, 128, _P, 128, 4, 32, 128, _P, 32, None), 1),
+    (lambda h: h.lm_linear(None, 128, _P, 128, 4, 32, 128, _P, 32, None), 1),
+    (lambda h: h.lm_linear(None, 128, None, 128, 0, 32, 128, None, 32, None), 0),
 ])
 def test_invalid_arguments_rejected_on_host(call, expected):
     assert call(_lib.load()) == expected
-
-
-# Non-null dummy pointers: every case returns before any launch, so nothing
-# is dereferenced (the checks run on the host only).
-_P = 16
 
 
 @pytest.mark.parametrize("name,call,expected", [

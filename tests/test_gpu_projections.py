@@ -90,6 +90,66 @@ def test_linear_splitk_frag_equals_row_major(rows, n, k):
         assert torch.equal(linear.linear_splitk_frag(junk, w, splits), linear.linear_splitk(a, w, splits))
 
 
+def _fp32_product(a, w, chunk=8192):
+    """fp32 product of the same bf16 operands (on the device, in row chunks)."""
+    wt = w.float().T
+    return torch.cat([a[i:i + chunk].float() @ wt for i in range(0, a.shape[0], chunk)])
+
+
+@pytest.mark.parametrize("rows,n,k", [
+    (46990, 2560, 1536),   # cfg 4 packed QKV (46,990 prefill tokens)
+    (46990, 1536, 1536),   # cfg 4 o_proj
+    (65536, 2560, 1536),   # cfg 3 prefill QKV (64 prompts of 1024)
+    (48, 49155, 1536),     # prefill LM head at the last positions: odd vocabulary, 2-byte stores
+    (1, 512, 1024), (17, 200, 256), (130, 2560, 1536), (257, 1536, 1536)])
+@torch.inference_mode()
+def test_linear_dense_matches_fp32_product(rows, n, k):
+    """lm_linear against an fp32 product of the same bf16 operands: the bf16
+    output within one ulp (or 1e-3 absolutely where the sum cancels)."""
+    g = torch.Generator(device=DEV).manual_seed(rows + n + k)
+    a = torch.randn(rows, k, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    got = linear.linear_dense(a, w)
+    exp = _fp32_product(a, w)
+    assert torch.isfinite(got.float()).all()
+    # fp32 accumulation-order error of a K-long sum of products of magnitude ~0.02
+    assert (got.float() - exp).abs().max() <= 1e-2 * exp.abs().max() or within_ulp_or_abs(
+        got, exp.to(torch.bfloat16), 1, 1e-3)
+    assert within_ulp_or_abs(got, exp.to(torch.bfloat16), 1, 1e-3)
+
+
+@torch.inference_mode()
+def test_linear_dense_is_batch_and_launch_invariant():
+    """A row's output is the same bits alone, inside any batch, at any row
+    position, through strided views, and on every launch (one workgroup
+    reduces each output over K in one order)."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    a = torch.randn(3000, 1536, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(2560, 1536, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    full = linear.linear_dense(a, w)
+    for _ in range(3):
+        assert torch.equal(linear.linear_dense(a, w), full)
+    for start, stop in ((0, 1), (5, 6), (100, 229), (2999, 3000), (1000, 2500)):
+        assert torch.equal(linear.linear_dense(a[start:stop], w), full[start:stop])
+    # strided input and output, and a weight that is a row range of a larger matrix
+    wide = torch.zeros(64, 2048, device=DEV, dtype=torch.bfloat16)
+    wide[:, 256:1792] = a[:64]
+    out = torch.full((64, 3000), float("nan"), device=DEV, dtype=torch.bfloat16)
+    linear.linear_dense(wide[:, 256:1792], w[512:2048], out=out[:, 100:1636])
+    assert torch.equal(out[:, 100:1636], full[:64, 512:2048])
+    assert out[:, :100].isnan().all() and out[:, 1636:].isnan().all()
+
+
+@torch.inference_mode()
+def test_linear_dense_rejections():
+    a = bf((16, 96)).to(DEV)
+    with pytest.raises(ValueError):
+        linear.linear_dense(a, bf((32, 96)).to(DEV))  # K not a multiple of 64
+    with pytest.raises(ValueError):
+        linear.linear_dense(bf((16, 128)).to(DEV), bf((32, 64)).to(DEV))
+    assert linear.linear_dense(bf((0, 128)).to(DEV), bf((32, 128)).to(DEV)).shape == (0, 32)
+
+
 def _qkv_case(b, hq, hkv, cap, splits, seed):
     g = torch.Generator().manual_seed(seed)
     ncols = (hq + 2 * hkv) * 64

@@ -83,7 +83,7 @@ def test_policy_key_and_restore_on_failure():
     """Reference test_fused_norm.py:15-48 / test_moe_finish.py:8-17: changing a
     captured policy requires a new engine; flags are restored on exit/failure."""
     from litemoe_amd.optimized import optimized_policy
-    model = SimpleNamespace(decode_flash=None, decode_lean=False,
+    model = SimpleNamespace(decode_flash=None, decode_lean=False, prefill_lean=False,
                             ep=SimpleNamespace(decode_lean=False, backend=SimpleNamespace(native=True, fused_combine=True)),
                             w={"layers": [{"logical": torch.empty(0)}]})
     run = SimpleNamespace(model=model, world=1, requests=[SimpleNamespace(prompt=[1, 2], budget=3)], capacity=8,
@@ -91,9 +91,9 @@ def test_policy_key_and_restore_on_failure():
     with pytest.raises(RuntimeError, match="injected"):
         with optimized_policy(run):
             with optimized_policy(run):
-                assert model.decode_lean and model.decode_flash == "flash"
+                assert model.decode_lean and model.decode_flash == "flash" and model.prefill_lean
             raise RuntimeError("injected")
-    assert not model.decode_lean and model.decode_flash is None
+    assert not model.decode_lean and model.decode_flash is None and not model.prefill_lean
     with optimized_policy(run):
         run.graph = object()
     run.flash_decode = False
@@ -188,3 +188,38 @@ def test_graph_recording_runs_with_the_collector_off():
         assert not gc.isenabled()  # a caller that had it off keeps it off
     finally:
         gc.enable()
+
+
+def test_capacity_zero_chooses_like_none():
+    """The reference picks a capacity for any falsy value (`capacity or ...`,
+    litemoe/engine.py:47): 0 and None give the same plan."""
+    from litemoe_amd.engine import plan_requests
+    from litemoe_amd.engine import Request
+    cfg = preset("granite-1b", num_hidden_layers=1, vocab_size=50)
+    reqs = [Request("a", [1, 2, 3], 4), Request("b", [5], 2)]
+    for mode in ("eager", "graph"):
+        assert plan_requests(reqs, cfg, mode, 0, 4096).capacity == plan_requests(reqs, cfg, mode, None, 4096).capacity
+    assert plan_requests(reqs, cfg, "eager", 0, 4096).capacity == 6
+    assert plan_requests(reqs, cfg, "graph", 0, 4096).capacity == 8
+
+
+def test_output_ring_dropped_during_capture_is_parked(monkeypatch):
+    """A ring freed while a stream capture runs keeps its pinned slots and
+    events alive (their release is a runtime call a capture forbids) until
+    release_parked() runs outside the capture."""
+    from litemoe_amd import execution
+    host, events = object(), [object(), object()]
+    ring = execution.OutputRing.__new__(execution.OutputRing)
+    ring.asynchronous, ring.host, ring.events = True, host, events
+    monkeypatch.setattr(execution, "_capturing", lambda: True)
+    del ring
+    assert execution._PARKED and execution._PARKED[-1] == (host, events)
+    execution.release_parked()  # still capturing: kept
+    assert execution._PARKED
+    monkeypatch.setattr(execution, "_capturing", lambda: False)
+    execution.release_parked()
+    assert execution._PARKED == []
+    ring = execution.OutputRing.__new__(execution.OutputRing)
+    ring.asynchronous, ring.host, ring.events = True, host, events
+    del ring  # outside a capture: freed at once
+    assert execution._PARKED == []
