@@ -4,7 +4,7 @@
 //   down:    y[r, n]   = bf16(act[r] . W2[e, n])
 //
 // over the route blocks of lm_moe_align (routes sorted by expert; a block is
-// at most 128 routes of one expert, found on the device from the offsets).
+// at most kTM routes of one expert, found on the device from the offsets).
 // y is in route order r = t*topk + branch, as on the decode path; act is in
 // route order for the public gate_up / down entry points and in sorted order
 // (row = position in the expert-sorted route list) between the two GEMMs of
@@ -12,11 +12,12 @@
 // contiguous run instead of gathering 128-byte pieces of rows spread over
 // the whole buffer.
 //
-// Workgroup = (output column tile, route block), 4 waves. It computes a
-// kTM x kTN fp32 tile (128 x 128 by default): for gate_up the B tile is
-// kTN/2 gate rows and the kTN/2 up rows of the same j, so silu(g)*u is
-// formed in registers. The waves sit in 2 x 2, each (kTM/2) x (kTN/2) as
-// 16 x 16 tiles of v_mfma_f32_16x16x32_bf16.
+// Workgroup = (output column tile, route block). It computes a kTM x kTN
+// fp32 tile (256 x 256 on 8 waves, or 128 x 128 on 4, see LargeTile /
+// SmallTile): for gate_up the B tile is kTN/2 gate rows and the kTN/2 up rows
+// of the same j, so silu(g)*u is formed in registers. The waves sit in
+// kWM x kWN, each (kTM/kWM) x (kTN/kWN) as 16 x 16 tiles of
+// v_mfma_f32_16x16x32_bf16.
 //
 // K runs in steps of 64: the next step's A rows (gathered through the route
 // list) and B rows are loaded into registers while the MFMAs run on the
@@ -39,29 +40,29 @@ namespace lm {
 namespace {
 
 constexpr int kBK = 64;   // K per stage
-constexpr int kThreads = 256;
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 constexpr int kRowBytes = kBK * 2;  // 128
 
-// Workgroup tile: kTM route rows x kTN B rows (output columns), with one
-// or two LDS stages. Measured at 65k tokens (3B shape): 128 x 128 with one
-// LDS stage (33 KB, three workgroups per CU) 3.34 ms for the MoE; with two
-// stages (two per CU) 3.83 ms; 256 x 256 (one per CU, accumulators in AGPRs)
-// 4.16 ms. At cfg 4 (47k tokens) 256 x 128 on eight waves (the same 64 x 64
-// wave tiles, one workgroup per CU) 2.79 against 2.52 ms; four workgroups per
-// CU of 128 x 128 need 128 registers and spill. More waves per CU beat the
-// lower LDS and L2 traffic per MFMA of the larger tile.
-#ifndef LM_EXPERT_GEMM_TM
-#define LM_EXPERT_GEMM_TM 128
-#endif
-#ifndef LM_EXPERT_GEMM_TN
-#define LM_EXPERT_GEMM_TN 128
-#endif
-#ifndef LM_EXPERT_GEMM_LDS_STAGES
-#define LM_EXPERT_GEMM_LDS_STAGES 1
-#endif
-constexpr int kTileM = LM_EXPERT_GEMM_TM, kTileN = LM_EXPERT_GEMM_TN;
-constexpr int kLdsStages = LM_EXPERT_GEMM_LDS_STAGES;
+// Two workgroup tiles, chosen per call by the routes per expert:
+// - Large: 256 route rows x 256 B rows on 8 waves of 64 x 128 (4 x 2), two
+//   LDS stages (128 KB, one workgroup per CU): a wave's fragments feed 32
+//   MFMAs per 32-wide k step, half the LDS reads per MFMA of a 64 x 64 wave
+//   tile. At cfg 4's 46,990 tokens (uniform routes, one box): gate/up 1230
+//   against 1561 us, down 912 against 1063 us for the small tile; 16 waves of
+//   64 x 64 1339 / 936 us, 128 x 256 on 8 waves 1412 / 1071 us.
+// - Small: 128 x 128 on 4 waves of 64 x 64, one LDS stage (33 KB, several
+//   workgroups per CU), for fewer than 1024 routes per expert, where a
+//   256-route block would be mostly padding.
+// (Earlier measurements of this kernel at 65k tokens: 128 x 128 with two
+// stages 3.83 against 3.34 ms for the MoE; 256 x 256 on 4 waves with the
+// accumulators in AGPRs 4.16 ms.)
+template <int TM, int TN, int WMv, int WNv, int StagesV>
+struct TileCfg {
+  static constexpr int M = TM, N = TN, WM = WMv, WN = WNv, Stages = StagesV;
+};
+using LargeTile = TileCfg<256, 256, 4, 2, 2>;
+using SmallTile = TileCfg<128, 128, 2, 2, 1>;
+constexpr int64_t kLargeTileRoutesPerExpert = 1024;
 
 // Block b of the per-expert blocks of bm routes (offsets: exclusive prefix
 // of per-expert counts, as lm_moe_align writes it), found by each wave with
@@ -105,21 +106,25 @@ __device__ __forceinline__ int frag_offset(int row, int chunk) {
 
 // kGateUp: B rows [0, kTN/2) are W13[e, j0 + r], [kTN/2, kTN) are
 // W13[e, I + j0 + r - kTN/2], output act; otherwise B rows are W2[e, n0 + r],
-// output y. Waves sit in 2 x 2; wave (wr, wc) owns rows wr*kTM/2 .. and, for
-// gate_up, gate and up rows of the same kTN/4 columns j.
+// output y. Waves sit in kWM x kWN; wave (wr, wc) owns rows wr*kTM/kWM .. and,
+// for gate_up, the gate and up rows of the same kTN/(2*kWN) columns j.
 // kPacked: weights in the fragment layout of lm_expert_pack (a load
 // instruction then reads eight whole 128-byte runs: the 8 rows of one
 // (k-step, k-group) are adjacent there).
 // kSortedAct: act row of sorted position p is p (gate_up writes, down reads).
-template <bool kGateUp, int kTM, int kTN, int kStages, bool kPacked, bool kSortedAct>
-__global__ void __launch_bounds__(kThreads, kTM * kTN > 128 * 128 ? 1 : 4 - kStages)
+template <bool kGateUp, int kTM, int kTN, int kWM, int kWN, int kStages, bool kPacked,
+          bool kSortedAct>
+__global__ void __launch_bounds__(64 * kWM * kWN)
 expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
                    const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted,
                    int topk, int K, int out_cols, int inter, int experts,
                    bf16 *__restrict__ out) {
-  constexpr int kWaveRows = kTM / 2;             // rows of a wave's tile
-  constexpr int kRB = kWaveRows / 16, kCB = kTN / 32;  // 16-row / 16-column blocks per wave
-  constexpr int kLA = kTM / 32, kLB = kTN / 32;  // 16-byte loads per lane per operand
+  constexpr int kWaves = kWM * kWN, kThreadsT = 64 * kWaves;
+  constexpr int kWaveRows = kTM / kWM, kWaveCols = kTN / kWN;
+  constexpr int kRB = kWaveRows / 16, kCB = kWaveCols / 16;  // 16-row / 16-column blocks per wave
+  constexpr int kLA = kTM / (8 * kWaves), kLB = kTN / (8 * kWaves);  // 16-byte loads per lane
+  static_assert(kLA * 8 * kWaves == kTM && kLB * 8 * kWaves == kTN, "tile rows per load round");
+  static_assert(!kGateUp || kCB % 2 == 0, "gate/up waves hold gate and up blocks in pairs");
   constexpr int kABytes = kTM * kRowBytes, kStageBytes = (kTM + kTN) * kRowBytes;
   __shared__ __align__(16) char smem[kStages * kStageBytes];
   __shared__ int route_of[kTM];
@@ -137,7 +142,7 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   if (!block_of(offsets, experts, kTM, tile_y, e, r0, r1)) return;
   const int n = r1 - r0;
   const int c0 = tile_x * (kGateUp ? kTN / 2 : kTN);  // first output column
-  for (int t = threadIdx.x; t < kTM; t += kThreads) route_of[t] = sorted[r0 + min(t, n - 1)];
+  for (int t = threadIdx.x; t < kTM; t += kThreadsT) route_of[t] = sorted[r0 + min(t, n - 1)];
   __syncthreads();
 
   // Load instruction i of wave w fills LDS rows 8*(w*L+i) .. +7 of an
@@ -165,7 +170,8 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   // element advance of one kBK step of B (two 32-wide k-steps when packed)
   constexpr int kBStep = kPacked ? (int)(kBK / 32 * wstep<true>()) : kBK;
   // One register stage: step k+1 is loaded while step k is computed from
-  // LDS, then stored to the other LDS buffer.
+  // LDS, then stored to the other LDS buffer (two stages) or to the same one
+  // after a barrier (one stage).
   u32x4 ra[kLA], rbv[kLB];
   auto load = [&](int kt) {
     const int k0 = kt * kBK;
@@ -183,14 +189,15 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
       *reinterpret_cast<u32x4 *>(base + kABytes + (wave * kLB + i) * 1024) = rbv[i];
   };
 
-  const int wr = wave / 2, wc = wave % 2;
+  const int wr = wave / kWN, wc = wave % kWN;
   const int fr = lane % 16, fk = lane / 16;
+  constexpr int kGateCols = kWaveCols / 2;  // gate/up: gate (and up) columns of a wave
   int brow[kCB];
 #pragma unroll
   for (int cb = 0; cb < kCB; ++cb)
-    brow[cb] = kGateUp ? (cb < kCB / 2 ? wc * (kTN / 4) + cb * 16
-                                       : kTN / 2 + wc * (kTN / 4) + (cb - kCB / 2) * 16)
-                       : wc * (kTN / 2) + cb * 16;
+    brow[cb] = kGateUp ? (cb < kCB / 2 ? wc * kGateCols + cb * 16
+                                       : kTN / 2 + wc * kGateCols + (cb - kCB / 2) * 16)
+                       : wc * kWaveCols + cb * 16;
   f32x4 acc[kRB][kCB];
 #pragma unroll
   for (int i = 0; i < kRB; ++i)
@@ -256,12 +263,12 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           h[i] = round_bf16_nc(silu(round_bf16_nc(acc[rb][cb][i]))) * round_bf16_nc(acc[rb][cb + kCB / 2][i]);
-        *reinterpret_cast<uint2 *>(o + wc * (kTN / 4) + cb * 16) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
+        *reinterpret_cast<uint2 *>(o + wc * kGateCols + cb * 16) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
       }
     } else {
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb)
-        *reinterpret_cast<uint2 *>(o + wc * (kTN / 2) + cb * 16) =
+        *reinterpret_cast<uint2 *>(o + wc * kWaveCols + cb * 16) =
             make_uint2(pack_bf16(acc[rb][cb][0], acc[rb][cb][1]), pack_bf16(acc[rb][cb][2], acc[rb][cb][3]));
     }
   }
@@ -273,54 +280,65 @@ bool expert_gemm_ok(int64_t routes, int64_t hidden, int64_t inter, int64_t exper
   // 32-bit element offsets: the gathered rows and the weights stay below 2^31.
   const int64_t rows = std::max(routes, experts * std::max(2 * inter, hidden));
   return routes >= kExpertGemmMinRoutes && hidden % kBK == 0 && inter % kBK == 0 &&
-         (2 * inter) % kTileN == 0 && hidden % kTileN == 0 &&
+         (2 * inter) % SmallTile::N == 0 && hidden % SmallTile::N == 0 &&
          rows * std::max(hidden, inter) < ((int64_t)1 << 31);
 }
+
+namespace {
+
+template <class T>
+int launch_tile(bool gate_up, const bf16 *a, const bf16 *w, const int32_t *offsets,
+                const int32_t *sorted, int64_t routes, int64_t topk, int64_t K, int64_t out_cols,
+                int64_t inter, int64_t experts, bf16 *out, bool packed, bool sorted_act,
+                hipStream_t stream) {
+  const int64_t blocks = align_up(cdiv(routes, T::M) + experts, kXcds);
+  if (blocks > 65535) return LM_EUNSUPPORTED;
+  const int64_t cols = gate_up ? 2 * inter : out_cols;
+  const dim3 grid((unsigned)(cols / T::N), (unsigned)blocks);
+  const int threads = 64 * T::WM * T::WN;
+  auto go = [&](auto gate_c, auto packed_c, auto sorted_c) {
+    expert_gemm_kernel<decltype(gate_c)::value, T::M, T::N, T::WM, T::WN, T::Stages,
+                       decltype(packed_c)::value, decltype(sorted_c)::value>
+        <<<grid, threads, 0, stream>>>(a, w, offsets, sorted, (int)topk, (int)K, (int)out_cols,
+                                       (int)inter, (int)experts, out);
+  };
+  using Y = std::true_type;
+  using F = std::false_type;
+  auto by_layout = [&](auto gate_c) {
+    if (packed) {
+      if (sorted_act) go(gate_c, Y{}, Y{}); else go(gate_c, Y{}, F{});
+    } else {
+      if (sorted_act) go(gate_c, F{}, Y{}); else go(gate_c, F{}, F{});
+    }
+  };
+  if (gate_up) by_layout(Y{}); else by_layout(F{});
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+bool large_tile(int64_t routes, int64_t hidden, int64_t inter, int64_t experts) {
+  return routes >= kLargeTileRoutesPerExpert * experts && (2 * inter) % LargeTile::N == 0 &&
+         hidden % LargeTile::N == 0;
+}
+
+}  // namespace
 
 int launch_expert_gemm_gate_up(const bf16 *x, const bf16 *w13, const int32_t *offsets,
                                const int32_t *sorted, int64_t routes, int64_t topk, int64_t hidden,
                                int64_t inter, int64_t experts, bf16 *act, bool packed,
                                bool sorted_act, hipStream_t stream) {
-  const int64_t blocks = align_up(cdiv(routes, kTileM) + experts, kXcds);
-  if (blocks > 65535) return LM_EUNSUPPORTED;
-  const dim3 grid((unsigned)(2 * inter / kTileN), (unsigned)blocks);
-  auto go = [&](auto packed_c, auto sorted_c) {
-    expert_gemm_kernel<true, kTileM, kTileN, kLdsStages, decltype(packed_c)::value,
-                       decltype(sorted_c)::value><<<grid, kThreads, 0, stream>>>(
-        x, w13, offsets, sorted, (int)topk, (int)hidden, (int)inter, (int)inter, (int)experts, act);
-  };
-  using T = std::true_type;
-  using F = std::false_type;
-  if (packed) {
-    if (sorted_act) go(T{}, T{}); else go(T{}, F{});
-  } else {
-    if (sorted_act) go(F{}, T{}); else go(F{}, F{});
-  }
-  LM_CHECK_LAUNCH();
-  return LM_OK;
+  auto launch = large_tile(routes, hidden, inter, experts) ? launch_tile<LargeTile> : launch_tile<SmallTile>;
+  return launch(true, x, w13, offsets, sorted, routes, topk, hidden, inter, inter, experts, act,
+                packed, sorted_act, stream);
 }
 
 int launch_expert_gemm_down(const bf16 *act, const bf16 *w2, const int32_t *offsets,
                             const int32_t *sorted, int64_t routes, int64_t hidden, int64_t inter,
                             int64_t experts, bf16 *y, bool packed, bool sorted_act,
                             hipStream_t stream) {
-  const int64_t blocks = align_up(cdiv(routes, kTileM) + experts, kXcds);
-  if (blocks > 65535) return LM_EUNSUPPORTED;
-  const dim3 grid((unsigned)(hidden / kTileN), (unsigned)blocks);
-  auto go = [&](auto packed_c, auto sorted_c) {
-    expert_gemm_kernel<false, kTileM, kTileN, kLdsStages, decltype(packed_c)::value,
-                       decltype(sorted_c)::value><<<grid, kThreads, 0, stream>>>(
-        act, w2, offsets, sorted, 1, (int)inter, (int)hidden, (int)inter, (int)experts, y);
-  };
-  using T = std::true_type;
-  using F = std::false_type;
-  if (packed) {
-    if (sorted_act) go(T{}, T{}); else go(T{}, F{});
-  } else {
-    if (sorted_act) go(F{}, T{}); else go(F{}, F{});
-  }
-  LM_CHECK_LAUNCH();
-  return LM_OK;
+  auto launch = large_tile(routes, hidden, inter, experts) ? launch_tile<LargeTile> : launch_tile<SmallTile>;
+  return launch(false, act, w2, offsets, sorted, routes, 1, inter, hidden, inter, experts, y, packed,
+                sorted_act, stream);
 }
 
 }  // namespace lm

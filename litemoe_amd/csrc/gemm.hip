@@ -13,9 +13,9 @@
 // eager or replayed from a graph (no split-K partials, no atomics, no stream-K
 // fix-up whose summation order the caller cannot see).
 //
-// Workgroup = kTM x kTN output tile (256 x 256 or 128 x 128), kWM x kWN
-// waves, each wave a (kTM/kWM) x (kTN/kWN) block of 16 x 16 MFMA tiles; K
-// runs in steps of 64.
+// Workgroup = kTM x kTN output tile (256 x 256 on 16 waves, or 128 x 128 on
+// 4), kWM x kWN waves, each wave a (kTM/kWM) x (kTN/kWN) block of 16 x 16
+// MFMA tiles; K runs in steps of 64.
 // The next step's A and B rows are loaded into registers while the MFMAs run
 // on the current step's LDS tile, then stored into the other of two LDS
 // buffers (one barrier per step). An LDS row is 64 bf16 = 8 chunks of 16
@@ -197,15 +197,15 @@ bool gemm_shape_ok(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
          (N - 1) * ldw + K < lim && tiles < lim;
 }
 
-// Prefill-sized row counts take 256 x 256 tiles (eight waves of 64 x 128:
-// half the LDS reads per MFMA of 64 x 64 wave tiles); measured at the cfg 4
-// QKV shape (46,990 x 1536 x 2560) 426 us against 582 us for 128 x 128 tiles
-// (two workgroups per CU) and 494-635 us for 128 x 256 / 256 x 128. Fewer rows
-// keep 128 x 128 tiles, whose grid spreads over more CUs.
+// Prefill-sized row counts take 256 x 256 tiles on 16 waves of 64 x 64 (four
+// waves per SIMD). On one box at the cfg 4 QKV shape (46,990 x 1536 x 2560):
+// 443 us against 509 us for 8 waves of 64 x 128 (two per SIMD), 539-587 us
+// for 128 x 256 / 256 x 128 on 16 waves; at the o_proj shape 280 against
+// 326 us. Fewer rows keep 128 x 128 tiles, whose grid spreads over more CUs.
 int launch_gemm(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16 *out, int64_t ldo,
                 int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   if (M >= 2048)
-    return launch_gemm_cfg<256, 256, 4, 2>(a, lda, w, ldw, out, ldo, M, N, K, stream);
+    return launch_gemm_cfg<256, 256, 4, 4>(a, lda, w, ldw, out, ldo, M, N, K, stream);
   return launch_gemm_cfg<128, 128, 2, 2>(a, lda, w, ldw, out, ldo, M, N, K, stream);
 }
 

@@ -311,13 +311,15 @@ def test_fused_experts_block_rows_do_not_change_results():
 
 
 @pytest.mark.parametrize("m,h,i,e,k,skew", [(2048, 256, 128, 64, 8, False), (2048, 256, 128, 64, 8, True),
-                                            (1100, 512, 256, 20, 4, False)])
+                                            (1100, 512, 256, 20, 4, False),
+                                            (8192, 256, 128, 16, 8, False), (8192, 256, 128, 16, 8, True)])
 @torch.inference_mode()
 def test_prefill_expert_gemm_and_chunked_align_match_oracle(m, h, i, e, k, skew):
     """Prefill-sized route counts (>= 4096 routes): lm_moe_routes takes the
-    LDS-tiled MFMA GEMMs over 128-route blocks, and above 8192 routes the
-    chunked three-launch align. Route outputs against the oracle's per-route
-    expert math; skew puts most routes on two experts and leaves some empty."""
+    LDS-tiled MFMA GEMMs (128-route blocks; 256-route blocks from 1024 routes
+    per expert, the m=8192 cases), and above 8192 routes the chunked
+    three-launch align. Route outputs against the oracle's per-route expert
+    math; skew puts most routes on two experts and leaves some empty."""
     x, w1, w2, _, ids = _moe_inputs(m, h, i, e, k, 700 + m)
     if skew:
         g = torch.Generator().manual_seed(m)
