@@ -166,6 +166,53 @@ def moe_roofline(model, cfg, batch, reps):
                 gate_up_bytes=gate_up_bytes, fused_bytes=fused_bytes)
 
 
+def decode_attention_rate(engine, cfg, reps):
+    """The decode attention over the engine's own KV cache after the timed
+    steps (every layer once per replay of a HIP graph, so nothing is cached
+    between layers): ``lm_flash_decode`` with the step's split plan. Bytes:
+    the K and V of every used position, plus q and the output."""
+    import torch
+
+    from litemoe_amd.execution import no_collection_while_recording
+    dev = engine.cache.k.device
+    batch, hq, hkv, d = engine.batch, cfg.num_attention_heads, cfg.num_key_value_heads, 64
+    used = engine.state["length"].to(torch.int32)
+    gen = torch.Generator(device=dev).manual_seed(9)
+    q = torch.randn(batch, hq, 1, d, device=dev, generator=gen).to(torch.bfloat16)
+    zeros = torch.zeros(batch, dtype=torch.int64, device=dev)
+    active = torch.ones(batch, dtype=torch.bool, device=dev)
+    flash, cache = engine.flash_attention, engine.cache
+
+    def all_layers():
+        for layer in range(cfg.num_hidden_layers):
+            flash(q, cache.k[layer], cache.v[layer], zeros, active, cfg.attention_multiplier, used=used)
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        all_layers()
+        side.synchronize()
+        with no_collection_while_recording(), torch.cuda.graph(graph, stream=side):
+            all_layers()
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (reps * cfg.num_hidden_layers)
+    keys = int(used.sum())
+    nbytes = keys * hkv * d * 2 * 2 + 2 * batch * hq * d * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": "decode_kernel (lm_flash_decode)", "achieved": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "us_per_layer": round(us, 2), "bytes_per_layer": nbytes,
+            "mean_context": round(keys / batch, 1)}
+
+
 BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -553,6 +600,8 @@ def main():
 
         roof = moe_roofline(model, cfg, args.batch, args.roofline_reps)
         log(f"gate_up {roof['gate_up_us']:.1f} us/launch, fused MoE {roof['fused_us']:.1f} us/layer")
+        attention = decode_attention_rate(engine, cfg, args.roofline_reps)
+        log(f"decode attention {attention['us_per_layer']:.1f} us/layer at mean context {attention['mean_context']}")
 
         engine_tps = None
         if not args.no_engine:
@@ -594,10 +643,14 @@ def main():
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("gate_up_scan_kernel.granite3b_b64_decode.txt") if headline else None,
+                     "traffic_source": ("rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE of this kernel, calibrated on a copy, "
+                                        "read from profiles/gate_up_scan_kernel.granite3b_b64_decode.txt (not measured "
+                                        "in this run)") if headline else None,
                      "bytes_per_launch": int(roof["gate_up_bytes"]), "us_per_launch": round(roof["gate_up_us"], 2),
                      "active_experts": roof["active"]},
         "fused_moe": {"achieved": round(fused_gbs, 1), "unit": "GB/s", "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
                       "us_per_layer": round(roof["fused_us"], 2), "bytes_per_layer": int(roof["fused_bytes"])},
+        "decode_attention": attention,
         "engine_decode_tps": None if engine_tps is None else round(engine_tps, 1),
         "cpu_baseline": cpu,
     }
