@@ -68,6 +68,9 @@ def parse():
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-engine", action="store_true")
+    ap.add_argument("--chained", action="store_true",
+                    help="decode layers with the combine fused into the down projection and the next norm "
+                         "into the QKV projection (Granite.chain_combine)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="skip decode timing: run only the MoE kernel timing (for counter collection)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -110,9 +113,12 @@ def moe_roofline(model, cfg, batch, reps):
     z = torch.randn(batch, H, device=dev, generator=gen).to(torch.bfloat16)
     x = torch.randn(batch, H, device=dev, generator=gen).to(torch.bfloat16)
     z_out = torch.empty_like(z)
+    # the step's MoE: chained (ids in expert order, the combine and residual
+    # add in the down launch) or gate/up, down and combine+add+norm
+    chained = model._combine_chain(batch)
     per_layer = []
     for w in model.w["layers"]:
-        weights, ids = router.route(z, w["block_sparse_moe.router.layer"], k)
+        weights, ids = router.route(z, w["block_sparse_moe.router.layer"], k, id_order=chained)
         act = torch.empty(batch * k, I, device=dev, dtype=torch.bfloat16)
         y = torch.empty(batch * k, H, device=dev, dtype=torch.bfloat16)
         active = int(torch.unique(ids).numel())
@@ -132,10 +138,17 @@ def moe_roofline(model, cfg, batch, reps):
                       w[w13_key].data_ptr(), None, None, ids.data_ptr(), batch * k, k, H, I, E, 0,
                       act.data_ptr(), stream)
 
+    sumsq = torch.empty(batch, H // 64, device=dev, dtype=torch.float32)
+
     def moe_all():
         for w, weights, ids, act, y, _ in per_layer:
-            experts.moe_routes(z, w[w13_key], w[w2_key], ids, workspace=backend.workspace, y=y, packed=packed)
-            experts.finish_add_rmsnorm(y, ids, weights, x, r, w["post_attention_layernorm"], eps, z_out)
+            if chained:
+                backend.routes_combine(z, w[w13_key], w[w2_key], ids, weights, residual=x, alpha=r, sumsq=sumsq,
+                                       packed=packed)
+            else:
+                experts.moe_routes(z, w[w13_key], w[w2_key], ids, workspace=backend.workspace, y=y,
+                                   packed=packed)
+                experts.finish_add_rmsnorm(y, ids, weights, x, r, w["post_attention_layernorm"], eps, z_out)
 
     result = {}
     for name, fn in (("gate_up", gate_up_all), ("fused", moe_all)):
@@ -163,7 +176,7 @@ def moe_roofline(model, cfg, batch, reps):
     gate_up_bytes = active * 2 * I * H * 2 + batch * H * 2 + batch * k * I * 2
     fused_bytes = active * 3 * I * H * 2 + 2 * batch * H * 2 + batch * k * 8
     return dict(gate_up_us=result["gate_up"], fused_us=result["fused"], active=active,
-                gate_up_bytes=gate_up_bytes, fused_bytes=fused_bytes)
+                gate_up_bytes=gate_up_bytes, fused_bytes=fused_bytes, chained=chained)
 
 
 def decode_attention_rate(engine, cfg, reps):
@@ -563,6 +576,7 @@ def main():
     ep = ExpertParallel(1, 0, args.batch, cfg.hidden_size, cfg.num_experts_per_tok, torch.bfloat16, dev,
                         HipFusedExperts())
     model = Granite(cfg, w, ep, 4096)
+    model.chain_combine = args.chained
     prompts = synth.prompts(args.batch, args.prompt, cfg.vocab_size, 1)
     requests = [Request(str(i), p, args.new_tokens) for i, p in enumerate(prompts)]
     if args.roofline_only:
@@ -649,7 +663,10 @@ def main():
                      "bytes_per_launch": int(roof["gate_up_bytes"]), "us_per_launch": round(roof["gate_up_us"], 2),
                      "active_experts": roof["active"]},
         "fused_moe": {"achieved": round(fused_gbs, 1), "unit": "GB/s", "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
-                      "us_per_layer": round(roof["fused_us"], 2), "bytes_per_layer": int(roof["fused_bytes"])},
+                      "us_per_layer": round(roof["fused_us"], 2), "bytes_per_layer": int(roof["fused_bytes"]),
+                      "launches": ("gate/up; down with the combine and the residual add (the next norm is "
+                                   "formed by the QKV projection)") if roof["chained"] else
+                                  "gate/up; down; combine with the residual add and the next norm"},
         "decode_attention": attention,
         "engine_decode_tps": None if engine_tps is None else round(engine_tps, 1),
         "cpu_baseline": cpu,

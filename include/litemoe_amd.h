@@ -222,7 +222,11 @@ int lm_prefill_attention(const void *q, int64_t qs0, int64_t qs1,
  * tokens with hidden = 512*{1,2,3,4,6,8} and 16 < experts <= 64, MFMA tiles
  * of 16 tokens (the last tokens % 16 on the GEMV), so a logit can differ by
  * one bf16 ulp between the two, as between any two BLAS orders. The
- * selection is exact given the logits. */
+ * selection is exact given the logits. `renormalize` is a set of flags:
+ * bit 0 (1) softmax over the selection, else over every logit; bit 1 (2)
+ * each token's selection written in ascending expert id (weights alongside)
+ * instead of descending logit, the order lm_moe_routes_combine_packed sums
+ * in. The same for every router entry point below. */
 int lm_router(const void *x, const void *gate_weight, int64_t tokens,
               int64_t hidden, int64_t experts, int64_t topk, int renormalize,
               void *logits_out, float *topk_weights, int32_t *topk_ids,
@@ -372,6 +376,21 @@ int lm_linear_splitk_frag(const void *a_frag, const void *weight, int64_t rows,
                           int64_t out_features, int64_t in_features,
                           int64_t splits, float *partials, void *stream);
 
+/* lm_linear_splitk whose input is rmsnorm(x) with the norm formed on the
+ * fly: a[m][k] = bf16(bf16(x[m][k] * r_m) * norm_weight[k]),
+ * r_m = 1 / sqrt(S_m / in_features + eps), where S_m is summed from
+ * sumsq[m][0 .. in_features/64) (lm_moe_routes_combine with a residual) in
+ * lm_rmsnorm's reduction order, so a is bitwise lm_rmsnorm(x). Replaces the
+ * next layer's input norm (litemoe/model.py:106) and its packed QKV
+ * projection (:47-49) in one launch. x: [rows, in_features] bf16
+ * contiguous; in_features a multiple of 512 up to 2048; otherwise the limits
+ * of lm_linear_splitk. */
+int lm_linear_splitk_rmsnorm(const void *x, const float *sumsq,
+                             const void *norm_weight, float eps,
+                             const void *weight, int64_t rows,
+                             int64_t out_features, int64_t in_features,
+                             int64_t splits, float *partials, void *stream);
+
 /* out[m][n] = bf16(sum_s partials[s][m][n]), s ascending; out row stride ldo. */
 int lm_linear_splitk_reduce(const float *partials, int64_t splits, int64_t rows,
                             int64_t out_features, void *out, int64_t ldo,
@@ -488,6 +507,46 @@ int lm_moe_routes_packed(const void *x, const void *w13, const void *w2,
                          int64_t topk, int64_t block_rows, void *y,
                          void *workspace, int64_t workspace_bytes,
                          void *stream);
+
+/* Workspace for lm_moe_routes_combine[_packed]. */
+int lm_moe_routes_combine_workspace_size(int64_t tokens, int64_t topk,
+                                         int64_t hidden, int64_t inter,
+                                         int64_t experts, int64_t *bytes);
+
+/* The decode MoE in two launches: the gate/up projection, then the down
+ * projection with the weighted combine fused in (the last workgroup to finish
+ * a 64-column tile sums that tile's route terms, counted with device-scope
+ * atomics on counters in the workspace, which the call clears and leaves
+ * clear). Each token's ids must be in ascending expert id (the router's id
+ * order, `renormalize` bit 1): the sum then runs in the moe_finish order
+ * (ascending id*K + branch) and equals lm_moe_routes + lm_moe_finish bit for
+ * bit. Two forms:
+ *   residual == NULL: out[t] = bf16(sum_j bf16(bf16(y_tj) * bf16(w_tj)));
+ *   residual != NULL: residual[t] <- bf16(residual[t] + alpha * that bf16),
+ *     and sumsq[t][c] (fp32 [tokens, hidden/64]) = the sum of squares of the
+ *     new residual over columns 64c .. 64c+63, formed as lm_rmsnorm forms its
+ *     partial sums, so lm_linear_splitk_rmsnorm can finish the next RMSNorm
+ *     in the same order.
+ * Replaces `ep(...)` -> vLLM fused_experts (litemoe/ep.py:40-41) and, with a
+ * residual, also `x.add(y, alpha=residual_multiplier)` (model.py:122). Decode
+ * scan path only (tokens <= 256, tokens*topk <= 2048, hidden a multiple of
+ * 64, inter <= 1024, topk <= 8); otherwise LM_EUNSUPPORTED. The _packed form
+ * reads lm_expert_pack weights. Calls that overlap on one workspace race. */
+int lm_moe_routes_combine(const void *x, const void *w13, const void *w2,
+                          const int32_t *topk_ids, const float *topk_weights,
+                          int64_t tokens, int64_t hidden, int64_t inter,
+                          int64_t experts, int64_t topk, void *residual,
+                          float alpha, float *sumsq, void *out,
+                          void *workspace, int64_t workspace_bytes,
+                          void *stream);
+int lm_moe_routes_combine_packed(const void *x, const void *w13,
+                                 const void *w2, const int32_t *topk_ids,
+                                 const float *topk_weights, int64_t tokens,
+                                 int64_t hidden, int64_t inter,
+                                 int64_t experts, int64_t topk,
+                                 void *residual, float alpha, float *sumsq,
+                                 void *out, void *workspace,
+                                 int64_t workspace_bytes, void *stream);
 int lm_fused_experts_packed(const void *x, const void *w13, const void *w2,
                             const float *topk_weights,
                             const int32_t *topk_ids, const int64_t *logical,

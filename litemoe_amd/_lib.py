@@ -50,12 +50,18 @@ _SIGNATURES = {
     "lm_moe_down_packed": [_v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _v, _v],
     "lm_moe_routes_packed": [_v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v, _i64, _v],
     "lm_expert_pack": [_v, _v, _i64, _i64, _i64, _v, _v, _v],
+    "lm_moe_routes_combine_workspace_size": [_i64, _i64, _i64, _i64, _i64, C.POINTER(C.c_int64)],
+    "lm_moe_routes_combine": [_v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _v, _f32, _v, _v, _v, _i64,
+                              _v],
+    "lm_moe_routes_combine_packed": [_v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _v, _f32, _v, _v, _v,
+                                     _i64, _v],
     "lm_fused_experts_packed": [_v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64, _i64, _v, _v,
                                 _i64, _v],
     "lm_moe_finish_add_rmsnorm": [_v, _v, _v, _v, _v, _f32, _v, _f32, _v, _i64, _i64, _i64, _v],
     "lm_linear_splitk": [_v, _i64, _v, _i64, _i64, _i64, _i64, _v, _v],
     "lm_linear_splitk_frag": [_v, _v, _i64, _i64, _i64, _i64, _v, _v],
     "lm_linear_splitk_reduce": [_v, _i64, _i64, _i64, _v, _i64, _v],
+    "lm_linear_splitk_rmsnorm": [_v, _v, _v, _f32, _v, _i64, _i64, _i64, _i64, _v, _v],
     "lm_linear": [_v, _i64, _v, _i64, _i64, _i64, _i64, _v, _i64, _v],
     "lm_flash_decode_qkv": [_v, _i64, _v, _i64, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64,
                             _f32, _i64, _i64, _v, _v, _i64, _v],

@@ -36,34 +36,111 @@ __device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cas
 // kFragA: A is in the fragment order of frag_offset_rows (mb = MB), so each
 // A load reads 1 KB contiguously; lda is unused. Measured on the QKV shape
 // (64 rows, K 1536, 3 slices): 4.94 against 5.87 us per launch.
-template <int KW, int MB, bool kFragA>
+// kNorm: A is rmsnorm(x) (x row-major, lda = K), formed here from x, the
+// norm weight and the per-64-column sums of squares of x that
+// lm_moe_routes_combine wrote (sumsq [M, K/64]), in rmsnorm_kernel's order:
+// the tiles' sums are the 8-lane DPP sums of that kernel, summed here in its
+// tree (pairs of tiles, then four such pairs per wave, then the waves), so
+// A is bitwise the lm_rmsnorm output it replaces.
+struct NormIn {
+  const float *sumsq;  // [M, K / 64]
+  const bf16 *weight;  // [K]
+  float eps;
+};
+
+constexpr int kMaxNormTiles = 32;  // K <= 2048
+
+template <int KW, int MB, bool kFragA, bool kNorm = false>
 __global__ void __launch_bounds__(kThreads)
 splitk_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w, int M, int N,
-              int K, float *__restrict__ part) {
+              int K, float *__restrict__ part, NormIn norm) {
   __shared__ f32x4 red[kWaves][MB][2][kWave];
+  __shared__ float row_scale[kNorm ? kMaxRows : 1];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
   const int n0 = blockIdx.x * kTileN, s = blockIdx.y;
   const int k0 = (s * kWaves + wave) * KW * 32 + grp * 8;
   u32x4 b[2][KW], av[MB][KW];
+  // kNorm: the row sums, x and the norm weight are requested before the
+  // weights, so the norm is formed while the weights stream (vector loads
+  // complete in issue order).
+  const int ntiles = K / 64;
+  f32x4 gs[kNorm ? kMaxNormTiles / 4 : 1];
+  u32x4 nwv[kNorm ? KW : 1];
+  if constexpr (kNorm) {
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(norm.sumsq + (int64_t)min((int)threadIdx.x, M - 1) * ntiles);
+#pragma unroll
+    for (int q = 0; q < kMaxNormTiles / 4; ++q) gs[q] = src[min(q, ntiles / 4 - 1)];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const bf16 *ar = a + (int64_t)min(m * 16 + col, M - 1) * lda + k0;
+#pragma unroll
+      for (int t = 0; t < KW; ++t) av[m][t] = load16(ar + t * 32);
+    }
+#pragma unroll
+    for (int t = 0; t < KW; ++t) nwv[t] = load16(norm.weight + k0 + t * 32);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const bf16 *wr = w + (int64_t)(n0 + 16 * j + col) * K + k0;
 #pragma unroll
     for (int t = 0; t < KW; ++t) b[j][t] = load16(wr + t * 32);
   }
+  if constexpr (kNorm) {
+    __builtin_amdgcn_sched_barrier(0);
+    if ((int)threadIdx.x < M) {
+      float g[kMaxNormTiles];
 #pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    if constexpr (kFragA) {
-      // k step c of this wave is (s*4 + wave)*KW + t; lane l's 8 values of
-      // row m*16 + l%16, k group l/16 sit at ((c*MB + m)*64 + l)*8
-      const bf16 *ab = a + ((int64_t)(s * kWaves + wave) * KW * MB + m) * 512 + lane * 8;
+      for (int q = 0; q < kMaxNormTiles / 4; ++q)
 #pragma unroll
-      for (int t = 0; t < KW; ++t) av[m][t] = load16(ab + (int64_t)t * MB * 512);
-    } else {
-      const bf16 *ar = a + (int64_t)min(m * 16 + col, M - 1) * lda + k0;
+        for (int i = 0; i < 4; ++i) g[4 * q + i] = 4 * q + i < ntiles ? gs[q][i] : 0.f;
+      // rmsnorm_kernel: a 16-lane row adds its two 8-lane sums, a wave its
+      // four rows in order, the workgroup its four waves in order.
+      float waves[4];
 #pragma unroll
-      for (int t = 0; t < KW; ++t) av[m][t] = load16(ar + t * 32);
+      for (int wv = 0; wv < 4; ++wv) {
+        float rows4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rows4[r] = g[8 * wv + 2 * r] + g[8 * wv + 2 * r + 1];
+        waves[wv] = ((rows4[0] + rows4[1]) + rows4[2]) + rows4[3];
+      }
+      const float total = ((waves[0] + waves[1]) + waves[2]) + waves[3];
+      row_scale[threadIdx.x] = 1.0f / sqrtf(total / (float)K + norm.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const float sc = row_scale[min(m * 16 + col, M - 1)];
+#pragma unroll
+      for (int t = 0; t < KW; ++t) {
+        float f[8], g[8];
+        unpack8(av[m][t], f);
+        unpack8(nwv[t], g);
+        u32x4 z;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t xs = pack_bf16_nc(f[2 * i] * sc, f[2 * i + 1] * sc);  // bf16(x * r), two at once
+          z[i] = pack_bf16(lo_f32(xs) * g[2 * i], hi_f32(xs) * g[2 * i + 1]);
+        }
+        av[m][t] = z;
+      }
+    }
+  }
+  if constexpr (!kNorm) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      if constexpr (kFragA) {
+        // k step c of this wave is (s*4 + wave)*KW + t; lane l's 8 values of
+        // row m*16 + l%16, k group l/16 sit at ((c*MB + m)*64 + l)*8
+        const bf16 *ab = a + ((int64_t)(s * kWaves + wave) * KW * MB + m) * 512 + lane * 8;
+#pragma unroll
+        for (int t = 0; t < KW; ++t) av[m][t] = load16(ab + (int64_t)t * MB * 512);
+      } else {
+        const bf16 *ar = a + (int64_t)min(m * 16 + col, M - 1) * lda + k0;
+#pragma unroll
+        for (int t = 0; t < KW; ++t) av[m][t] = load16(ar + t * 32);
+      }
     }
   }
   f32x4 c[MB][2];
@@ -117,17 +194,18 @@ splitk_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
 
 int row_blocks(int64_t M) { return frag_row_blocks(M); }
 
-template <bool kFragA>
+template <bool kFragA, bool kNorm = false>
 int launch_splitk(const bf16 *a, int64_t lda, const bf16 *weight, int64_t rows,
                   int64_t out_features, int64_t in_features, int64_t splits, float *partials,
-                  hipStream_t s) {
+                  hipStream_t s, NormIn norm = NormIn{}) {
   const int kw = (int)(in_features / (splits * kWaves * 32));
   const dim3 grid((unsigned)(out_features / kTileN), (unsigned)splits);
   const int M = (int)rows, N = (int)out_features, K = (int)in_features;
   const int mb = row_blocks(rows);
 #define LM_SPLITK(KW, MB)                                                                          \
   if (kw == KW && mb == MB) {                                                                      \
-    splitk_kernel<KW, MB, kFragA><<<grid, kThreads, 0, s>>>(a, lda, weight, M, N, K, partials);    \
+    splitk_kernel<KW, MB, kFragA, kNorm><<<grid, kThreads, 0, s>>>(a, lda, weight, M, N, K, partials, \
+                                                                     norm);                       \
     LM_CHECK_LAUNCH();                                                                             \
     return LM_OK;                                                                                  \
   }
@@ -172,6 +250,22 @@ extern "C" int lm_linear_splitk_frag(const void *a_frag, const void *weight, int
   LM_REQUIRE(a_frag && weight && partials);
   return launch_splitk<true>((const bf16 *)a_frag, 0, (const bf16 *)weight, rows, out_features,
                              in_features, splits, partials, (hipStream_t)stream);
+}
+
+extern "C" int lm_linear_splitk_rmsnorm(const void *x, const float *sumsq, const void *norm_weight,
+                                        float eps, const void *weight, int64_t rows,
+                                        int64_t out_features, int64_t in_features, int64_t splits,
+                                        float *partials, void *stream) {
+  LM_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0 && splits > 0);
+  if (rows == 0) return LM_OK;
+  if (!splitk_shape_ok(rows, out_features, in_features, splits) || in_features % 512 ||
+      in_features / 64 > kMaxNormTiles)
+    return LM_EUNSUPPORTED;
+  LM_REQUIRE(x && sumsq && norm_weight && weight && partials);
+  return launch_splitk<false, true>((const bf16 *)x, in_features, (const bf16 *)weight, rows,
+                                    out_features, in_features, splits, partials,
+                                    (hipStream_t)stream,
+                                    NormIn{sumsq, (const bf16 *)norm_weight, eps});
 }
 
 extern "C" int lm_linear_splitk_reduce(const float *partials, int64_t splits, int64_t rows,

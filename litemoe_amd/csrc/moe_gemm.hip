@@ -247,7 +247,11 @@ template <int KS, bool kPacked>
 __global__ void __launch_bounds__(kThreads, KS <= 12 ? 4 : 2)
 gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
                     const int32_t *__restrict__ ids, int routes, int topk, int hidden, int inter,
-                    bf16 *__restrict__ act) {
+                    bf16 *__restrict__ act, int32_t *__restrict__ zero_counters, int counters) {
+  // The arrival counters of the following down launch start at zero (they
+  // are also left at zero by it): one workgroup clears them.
+  if (zero_counters && blockIdx.x == 0 && blockIdx.y == 0 && (int)threadIdx.x < counters)
+    zero_counters[threadIdx.x] = 0;
   __shared__ float red[kWaves][2][4][kWave];
   __shared__ int list[kScanList];
   __shared__ int wave_count[kWaves];
@@ -436,6 +440,119 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
   }
 }
 
+// The combine fused into the down projection (kFin 1 and 2 of
+// down_scan_kernel). Each workgroup writes, instead of its routes' y, the
+// weighted terms bf16(y * bf16(scale)) of the moe_finish sum; the last
+// workgroup to finish a column tile (counted with a device-scope atomic, one
+// counter per tile) sums the tokens' terms in branch order j = 0..topk-1
+// for that tile. A token's routes must be in ascending expert id (the
+// router's id order), which makes j the moe_finish order (logical id*K + j,
+// identity placement), so the sum is bitwise that of lm_moe_finish.
+//   kFin 1: out[t] = bf16(sum);
+//   kFin 2: x[t] <- bf16(x[t] + alpha * bf16(sum)) and sumsq[t][tile] = the
+//           tile's sum of squares of the new x in rmsnorm_kernel's order (the
+//           per-16-byte-word sums and the 8-lane DPP tree of wave_sum), from
+//           which lm_linear_splitk_rmsnorm finishes the next RMSNorm.
+// The terms cross XCDs (each XCD has its own L2): they are stored and loaded
+// at device scope (write-through stores, loads that do not trust a possibly
+// stale L2 line), each workgroup waits for its stores before it arrives, and
+// the last arriver loads only after its arrival returned.
+struct TileCombine {
+  int32_t *counters;       // [column tiles]; zero on entry, left zero
+  const float *scales;     // [tokens, topk]
+  bf16 *out;               // kFin 1: out [tokens, hidden]; kFin 2: the residual x, updated
+  float alpha;             // kFin 2
+  float *sumsq;            // kFin 2: [tokens, hidden / 64]
+  int tokens, topk;
+};
+
+__device__ __forceinline__ void store_dev32(bf16 *p, uint32_t v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A buffer resource over `bytes` bytes from `base` (raw buffer: no stride,
+// the gfx9 data-format word), for loads with explicit cache-policy bits.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes at `offset` with device scope (sc1: coherent across the XCDs' L2s).
+__device__ __forceinline__ u32x4 load_dev16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
+  constexpr int kDeviceScope = 16;  // cache-policy bit sc1
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)offset, 0, kDeviceScope);
+}
+
+// Wait until every vector memory operation of the wave has completed (the
+// device-scope term stores are then visible to every XCD): s_waitcnt
+// vmcnt(0) in gfx9's encoding (expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// The last arriver's sum for column tile `tile` (64 columns from n0): one
+// task per (token, 16-byte word), 8 consecutive lanes per token, so that
+// lanes 8g .. 8g+7 hold one token's 8 words as rmsnorm_kernel's lanes hold
+// them and dpp_sum8 forms the same partial sum.
+template <int kFin>
+__device__ void combine_tile(const TileCombine &c, const bf16 *__restrict__ terms, int hidden,
+                             int tile, int n0) {
+  constexpr int kMaxK = 8;
+  constexpr int kBatch = 2;  // tasks per thread whose loads are in flight together
+  const int ntiles = hidden / 64;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      buffer_over(terms, (uint32_t)((int64_t)c.tokens * c.topk * hidden * 2));
+  const int tasks = c.tokens * 8;
+  for (int base = 0; base < tasks; base += kBatch * kThreads) {
+    u32x4 tv[kBatch][kMaxK], xv[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int task = min(base + b * kThreads + (int)threadIdx.x, tasks - 1);
+      const int t = task >> 3, col = n0 + (task & 7) * 8;
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j)
+        tv[b][j] = load_dev16(rsrc, (uint32_t)((((int64_t)t * c.topk + min(j, c.topk - 1)) * hidden + col) * 2));
+      xv[b] = u32x4{0u, 0u, 0u, 0u};
+      if constexpr (kFin == 2) xv[b] = *reinterpret_cast<const u32x4 *>(c.out + (int64_t)t * hidden + col);
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int task = base + b * kThreads + (int)threadIdx.x;
+      const int t = min(task, tasks - 1) >> 3, wd = task & 7, col = n0 + wd * 8;
+      // Intermediate roundings skip the NaN fix-up (the stores canonicalize).
+      float total[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j) {
+        if (j < c.topk) {
+          float f[8];
+          unpack8(tv[b][j], f);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) total[q] += f[q];
+        }
+      }
+      u32x4 o;
+      if constexpr (kFin == 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = pack_bf16(total[2 * q], total[2 * q + 1]);
+        if (task < tasks) *reinterpret_cast<u32x4 *>(c.out + (int64_t)t * hidden + col) = o;
+      } else {
+        float xf[8], xn[8];
+        unpack8(xv[b], xf);
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          xn[q] = round_bf16_nc(xf[q] + c.alpha * round_bf16_nc(total[q]));
+          ss += xn[q] * xn[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = pack_bf16(xn[2 * q], xn[2 * q + 1]);
+        ss = dpp_sum8(ss);  // every lane of the group takes part (tasks come in whole groups)
+        if (task < tasks) {
+          *reinterpret_cast<u32x4 *>(c.out + (int64_t)t * hidden + col) = o;
+          if (wd == 0) c.sumsq[(int64_t)t * ntiles + tile] = ss;
+        }
+      }
+    }
+  }
+}
+
 // The decode scan path of the down projection as a kernel of its own, as
 // gate_up_scan_kernel is for gate/up: weights prefetched before the scan,
 // activation rows past the route set repeating its last route (no
@@ -443,15 +560,17 @@ down_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
 // workgroup covers NT MFMA tiles of 16 output columns (KS: 32-wide k steps
 // per wave, inter = KS * 32 * kWaves); its activation loads are issued back
 // to back. Same MFMA order and wave-order sum as down_kernel, hence the same
-// bits.
-template <int KS, int NT, bool kPacked>
+// bits. kFin: the combine fused in (TileCombine; NT == 4, 64-column tiles).
+template <int KS, int NT, bool kPacked, int kFin = 0>
 __global__ void __launch_bounds__(kThreads)
 down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
                  const int32_t *__restrict__ ids, int routes, int hidden, int inter,
-                 bf16 *__restrict__ y) {
+                 bf16 *__restrict__ y, TileCombine fin) {
+  static_assert(kFin == 0 || NT == 4, "the fused combine works on 64-column tiles");
   __shared__ float red[kWaves][NT][4][kWave];
   __shared__ int list[kScanList];
   __shared__ int wave_count[kWaves];
+  __shared__ int last_flag;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane % 16, grp = lane / 16;
   int e, tile;
@@ -470,11 +589,16 @@ down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
   }
   __builtin_amdgcn_sched_barrier(0);
   const int n = scan_ids(scan, e, list, wave_count);
-  if (n == 0) return;
   auto block = [&](int rb) {
     const bf16 *ar = act + (int64_t)list[min(rb + col, n - 1)] * inter + kbase;
 #pragma unroll
     for (int s = 0; s < KS; ++s) a[s] = load16(ar + s * 32);
+    // Wave w finishes C row 4*grp + w of every lane group (below); its
+    // route's scale is requested behind the activations.
+    const int row = rb + grp * 4 + wave;
+    const int route = list[min(row, n - 1)];
+    float sc = 0.f;
+    if constexpr (kFin != 0) sc = fin.scales[route];
     __builtin_amdgcn_sched_barrier(0);  // all activation loads in flight before the MFMAs
     f32x4 c[NT];
 #pragma unroll
@@ -488,22 +612,47 @@ down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
 #pragma unroll
       for (int i = 0; i < 4; ++i) red[wave][t][i][lane] = c[t][i];
     __syncthreads();
-    // Wave w finishes C row 4*grp + w of every lane group.
-    const int row = rb + grp * 4 + wave;
-    bf16 *yr = y + (int64_t)list[min(row, n - 1)] * hidden + n0 + col;
+    bf16 *yr = y + (int64_t)route * hidden + n0 + col;
+    sc = round_bf16_nc(sc);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       float v = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) v += red[w][t][wave][lane];
-      if (row < n) yr[16 * t] = (bf16)f32_to_bf16(v);
+      if constexpr (kFin == 0) {
+        if (row < n) yr[16 * t] = (bf16)f32_to_bf16(v);
+      } else {
+        // the moe_finish term bf16(bf16(y) * bf16(scale)); lanes col and
+        // col + 1 (DPP quad_perm [1,0,3,2]) store as one 4-byte word
+        const float term = round_bf16_nc(round_bf16_nc(v) * sc);
+        const float next = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(term), 0xB1, 0xF, 0xF, true));
+        if (row < n && (col & 1) == 0) store_dev32(yr + 16 * t, pack_bf16(term, next));
+      }
     }
     __syncthreads();
   };
-  if (n <= 16) {
-    block(0);
-  } else {
-    for (int rb = 0; rb < n; rb += 16) block(rb);
+  if (n > 0) {
+    if (n <= 16) {
+      block(0);
+    } else {
+      for (int rb = 0; rb < n; rb += 16) block(rb);
+    }
+  }
+  if constexpr (kFin != 0) {
+    // Every workgroup of the tile arrives once (an expert without routes
+    // too), after its term stores have completed.
+    wait_vector_memory();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int before = __hip_atomic_fetch_add(fin.counters + tile, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+      last_flag = before == (int)gridDim.y - 1;
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    if (threadIdx.x == 0)
+      __hip_atomic_store(fin.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    combine_tile<kFin>(fin, y, hidden, tile, n0);
   }
 }
 
@@ -561,7 +710,7 @@ int launch_gate_up_t(const bf16 *x, const bf16 *w13, const int32_t *offsets, con
   case KS:                                                                                      \
     if (mode == kScanPrefetch)                                                                  \
       gate_up_scan_kernel<KS, kPacked><<<grid, kThreads, 0, stream>>>(x, w13, ids, (int)routes,          \
-          (int)topk, (int)hidden, (int)inter, act);                                             \
+          (int)topk, (int)hidden, (int)inter, act, nullptr, 0);                                 \
     else if (mode == kScanLazy)                                                                 \
       gate_up_kernel<KS, kScanLazy, kPacked><<<grid, kThreads, 0, stream>>>(x, w13, offsets, sorted,     \
           ids, (int)routes, (int)topk, (int)hidden, (int)inter, (int)experts, bm, act);         \
@@ -599,7 +748,7 @@ int launch_down_t(const bf16 *act, const bf16 *w2, const int32_t *offsets, const
 #define X(KS)                                                                                  \
   case KS:                                                                                     \
     down_scan_kernel<KS, (kNT > 0 ? kNT : 1), kPacked><<<sgrid, kThreads, 0, stream>>>(                 \
-        act, w2, ids, (int)routes, (int)hidden, (int)inter, y);                                \
+        act, w2, ids, (int)routes, (int)hidden, (int)inter, y, TileCombine{});                 \
     LM_CHECK_LAUNCH();                                                                         \
     return LM_OK;
       X(1) X(2) X(3) X(4) X(6) X(8)
@@ -622,6 +771,51 @@ int launch_down_t(const bf16 *act, const bf16 *w2, const int32_t *offsets, const
           (int)routes, (int)hidden, (int)inter, (int)experts, bm, y);                          \
     break;
     LM_KS_LIST(X)
+#undef X
+    default:
+      return LM_EUNSUPPORTED;
+  }
+  LM_CHECK_LAUNCH();
+  return LM_OK;
+}
+
+// gate/up then down with the combine fused in, on the scan kernels (weights
+// prefetched before the route scan at every route count): LM_EUNSUPPORTED
+// where those kernels do not apply.
+template <bool kPacked>
+int launch_routes_combine_t(const bf16 *x, const bf16 *w13, const bf16 *w2, const int32_t *ids,
+                            int64_t tokens, int64_t topk, int64_t hidden, int64_t inter,
+                            int64_t experts, bf16 *act, bf16 *terms, const TileCombine &fin,
+                            bool residual, hipStream_t stream) {
+  const int64_t routes = tokens * topk;
+  if (hidden % 64 || hidden / 64 > kThreads || inter > 8 * 128 || experts > 65535)
+    return LM_EUNSUPPORTED;
+  const dim3 ggrid((unsigned)(inter / 16), (unsigned)experts);
+  const dim3 dgrid((unsigned)(hidden / 64), (unsigned)experts);
+  switch (hidden / 128) {
+#define X(KS)                                                                                      \
+  case KS:                                                                                         \
+    gate_up_scan_kernel<KS, kPacked><<<ggrid, kThreads, 0, stream>>>(                              \
+        x, w13, ids, (int)routes, (int)topk, (int)hidden, (int)inter, act, fin.counters,           \
+        (int)(hidden / 64));                                                                       \
+    break;
+    LM_KS_LIST(X)
+#undef X
+    default:
+      return LM_EUNSUPPORTED;
+  }
+  LM_CHECK_LAUNCH();
+  switch (inter / 128) {
+#define X(KS)                                                                                      \
+  case KS:                                                                                         \
+    if (residual)                                                                                  \
+      down_scan_kernel<KS, 4, kPacked, 2><<<dgrid, kThreads, 0, stream>>>(                         \
+          act, w2, ids, (int)routes, (int)hidden, (int)inter, terms, fin);                         \
+    else                                                                                           \
+      down_scan_kernel<KS, 4, kPacked, 1><<<dgrid, kThreads, 0, stream>>>(                         \
+          act, w2, ids, (int)routes, (int)hidden, (int)inter, terms, fin);                         \
+    break;
+    X(1) X(2) X(3) X(4) X(6) X(8)
 #undef X
     default:
       return LM_EUNSUPPORTED;
@@ -659,14 +853,16 @@ struct ExpertWorkspace {
   int32_t *offsets, *sorted, *align_scratch;
   int64_t align_bytes;
   bf16 *act, *y;
+  int32_t *counters;
   int64_t bytes;
 };
 
 // Layout: offsets [E+1], sorted [R] (block path only), the chunked align's
-// counts and bases (large R only), act [R, I], and (for lm_fused_experts)
-// y [R, H].
+// counts and bases (large R only), act [R, I], (for lm_fused_experts and the
+// combine entry points) y [R, H], and (combine entry points) the arrival
+// counters of the column tiles [H / 64].
 ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, int64_t inter,
-                      int64_t experts, bool with_y) {
+                      int64_t experts, bool with_y, bool with_counters = false) {
   const int64_t routes = tokens * topk;
   char *p = static_cast<char *>(base);
   ExpertWorkspace w;
@@ -682,6 +878,8 @@ ExpertWorkspace carve(void *base, int64_t tokens, int64_t topk, int64_t hidden, 
   off += align_up(2 * routes * inter, 256);
   w.y = with_y ? reinterpret_cast<bf16 *>(p + off) : nullptr;
   if (with_y) off += align_up(2 * routes * hidden, 256);
+  w.counters = with_counters ? reinterpret_cast<int32_t *>(p + off) : nullptr;
+  if (with_counters) off += align_up(4 * cdiv(hidden, 64), 256);
   w.bytes = off;
   return w;
 }
@@ -875,6 +1073,60 @@ extern "C" int lm_moe_routes_packed(const void *x, const void *w13, const void *
                                     int64_t workspace_bytes, void *stream) {
   return moe_routes(x, w13, w2, topk_ids, tokens, hidden, inter, experts, topk, block_rows, y,
                     workspace, workspace_bytes, true, stream);
+}
+
+extern "C" int lm_moe_routes_combine_workspace_size(int64_t tokens, int64_t topk, int64_t hidden,
+                                                    int64_t inter, int64_t experts, int64_t *bytes) {
+  LM_REQUIRE(bytes && tokens >= 0 && topk > 0 && hidden > 0 && inter > 0 && experts > 0);
+  *bytes = carve(nullptr, tokens, topk, hidden, inter, experts, true, true).bytes;
+  return LM_OK;
+}
+
+namespace {
+int moe_routes_combine(const void *x, const void *w13, const void *w2, const int32_t *topk_ids,
+                       const float *topk_weights, int64_t tokens, int64_t hidden, int64_t inter,
+                       int64_t experts, int64_t topk, void *residual, float alpha, float *sumsq,
+                       void *out, void *workspace, int64_t workspace_bytes, bool packed,
+                       void *stream) {
+  LM_REQUIRE(tokens >= 0 && topk > 0 && topk <= 8 && topk <= experts && experts <= 511);
+  if (!expert_shapes_ok(hidden, inter) || !scan_path(tokens, topk)) return LM_EUNSUPPORTED;
+  if (tokens == 0) return LM_OK;
+  LM_REQUIRE(x && w13 && w2 && topk_ids && topk_weights && workspace);
+  LM_REQUIRE(residual ? (sumsq != nullptr && out == nullptr) : (out != nullptr && sumsq == nullptr));
+  ExpertWorkspace w = carve(workspace, tokens, topk, hidden, inter, experts, true, true);
+  if (workspace_bytes < w.bytes) return LM_EWORKSPACE;
+  TileCombine fin;
+  fin.counters = w.counters;
+  fin.scales = topk_weights;
+  fin.out = (bf16 *)(residual ? residual : out);
+  fin.alpha = alpha;
+  fin.sumsq = sumsq;
+  fin.tokens = (int)tokens;
+  fin.topk = (int)topk;
+  auto launch = packed ? launch_routes_combine_t<true> : launch_routes_combine_t<false>;
+  return launch((const bf16 *)x, (const bf16 *)w13, (const bf16 *)w2, topk_ids, tokens, topk, hidden,
+                inter, experts, w.act, w.y, fin, residual != nullptr, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int lm_moe_routes_combine(const void *x, const void *w13, const void *w2,
+                                     const int32_t *topk_ids, const float *topk_weights,
+                                     int64_t tokens, int64_t hidden, int64_t inter,
+                                     int64_t experts, int64_t topk, void *residual, float alpha,
+                                     float *sumsq, void *out, void *workspace,
+                                     int64_t workspace_bytes, void *stream) {
+  return moe_routes_combine(x, w13, w2, topk_ids, topk_weights, tokens, hidden, inter, experts, topk,
+                            residual, alpha, sumsq, out, workspace, workspace_bytes, false, stream);
+}
+
+extern "C" int lm_moe_routes_combine_packed(const void *x, const void *w13, const void *w2,
+                                            const int32_t *topk_ids, const float *topk_weights,
+                                            int64_t tokens, int64_t hidden, int64_t inter,
+                                            int64_t experts, int64_t topk, void *residual,
+                                            float alpha, float *sumsq, void *out, void *workspace,
+                                            int64_t workspace_bytes, void *stream) {
+  return moe_routes_combine(x, w13, w2, topk_ids, topk_weights, tokens, hidden, inter, experts, topk,
+                            residual, alpha, sumsq, out, workspace, workspace_bytes, true, stream);
 }
 
 extern "C" int lm_expert_pack(const void *w13, const void *w2, int64_t experts, int64_t hidden,

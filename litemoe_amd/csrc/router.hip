@@ -64,6 +64,12 @@ __device__ void router_gemv(const u32x4 *zs, const bf16 *__restrict__ wr, int nv
   }
 }
 
+// `renormalize` flags: bit 0, softmax over the selection (else over every
+// logit); bit 1 (kIdOrder), each token's selection written in ascending
+// expert id instead of descending logit (the same experts and weights; the
+// denominator is summed in rank order either way).
+constexpr int kIdOrder = 2;
+
 // Top-k by rank: thread t (one per expert) counts the experts with a larger
 // key; ranks are distinct, so rank < topk places expert t at that position.
 // Weights: softmax over the selection (renormalize) or over all logits,
@@ -85,13 +91,18 @@ __device__ void select_topk(const float *logit, int experts, int topk, int renor
   if (t < topk) {
     const float m = sel_val[0];
     float denom = 0.f;
-    if (renormalize) {
+    if (renormalize & 1) {
       for (int j = 0; j < topk; ++j) denom += expf(sel_val[j] - m);
     } else {
       for (int e = 0; e < experts; ++e) denom += expf(logit[e] - m);
     }
-    tw[t] = expf(sel_val[t] - m) / denom;
-    tid[t] = sel_id[t];
+    int pos = t;
+    if (renormalize & kIdOrder) {
+      pos = 0;
+      for (int j = 0; j < topk; ++j) pos += sel_id[j] < sel_id[t];
+    }
+    tw[pos] = expf(sel_val[t] - m) / denom;
+    tid[pos] = sel_id[t];
   }
 }
 
@@ -140,7 +151,7 @@ __device__ void select_topk_lanes(const float *logit, float *scratch, int t, int
   const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
   const float ex = expf(v - m);
   float denom = 0.f;
-  if (renormalize) {
+  if (renormalize & 1) {
     if (rank < topk) terms[rank] = ex;
 #pragma unroll
     for (int r4 = 0; r4 < kMaxTopk / 4; ++r4) {
@@ -159,9 +170,12 @@ __device__ void select_topk_lanes(const float *logit, float *scratch, int t, int
       for (int i = 0; i < 4; ++i) denom += 4 * e4 + i < experts ? tv[i] : 0.f;
     }
   }
+  // kIdOrder: lane t's place among the selected lanes below it.
+  const uint64_t chosen = __ballot(rank < topk);
+  const int pos = (renormalize & kIdOrder) ? __popcll(chosen & ((1ull << t) - 1ull)) : rank;
   if (rank < topk) {
-    tw[rank] = ex / denom;
-    tid[rank] = t;
+    tw[pos] = ex / denom;
+    tid[pos] = t;
   }
 }
 

@@ -96,6 +96,12 @@ class HipFusedExperts:
                              global_num_experts, out=out, block_rows=self.block_rows,
                              workspace=self.workspace)
 
+    def routes_combine(self, x, w1, w2, topk_ids, topk_weights, residual=None, alpha=1.0, sumsq=None,
+                       packed=False):
+        """:func:`moe_routes_combine` on this backend's workspace."""
+        return moe_routes_combine(x, w1, w2, topk_ids, topk_weights, residual, alpha, sumsq,
+                                  workspace=self.workspace, packed=packed)
+
     def routes(self, x, w1, w2, topk_ids, packed=False):
         """Unweighted per-route expert outputs ``[M*k, H]`` in route order
         (``packed``: weights from :func:`pack_expert_weights`)."""
@@ -151,6 +157,49 @@ def moe_routes(x, w1, w2, topk_ids, block_rows=0, workspace=None, y=None, packed
               ids.data_ptr(), tokens, hidden, inter, experts, topk, block_rows, y.data_ptr(), ws.data_ptr(),
               ws.numel(), _lib.stream(x.device))
     return y
+
+
+def moe_routes_combine(x, w1, w2, topk_ids, topk_weights, residual=None, alpha=1.0, sumsq=None, out=None,
+                       workspace=None, packed=False):
+    """The decode MoE in two launches, the combine fused into the down
+    projection (``lm_moe_routes_combine``). Each token's ids must be in
+    ascending expert id (the router's ``id_order``). Without ``residual``:
+    returns ``out [M, H] = bf16(sum_j bf16(bf16(y_tj) * bf16(w_tj)))``
+    (equal to :func:`moe_routes` + ``moe_finish``). With ``residual``:
+    ``residual <- bf16(residual + alpha * out)`` in place, and returns
+    ``sumsq [M, H/64]`` fp32, the per-64-column sums of squares of the new
+    residual that :func:`linear.linear_splitk_rmsnorm` finishes the next
+    RMSNorm from."""
+    experts, hidden, inter = _check_weights(x, w1, w2)
+    tokens = x.numel() // hidden
+    ids = topk_ids.to(torch.int32).contiguous()
+    weights = topk_weights.to(torch.float32).contiguous()
+    topk = ids.shape[-1]
+    if ids.shape[0] != tokens or weights.shape != ids.shape:
+        raise ValueError('Router outputs must be [tokens, topk]')
+    if residual is not None:
+        if residual.shape != (tokens, hidden) or residual.dtype != torch.bfloat16 or not residual.is_contiguous():
+            raise ValueError('Residual must be contiguous bf16 [tokens, hidden]')
+        if sumsq is None:
+            sumsq = torch.empty(tokens, hidden // 64, device=x.device, dtype=torch.float32)
+        elif sumsq.shape != (tokens, hidden // 64) or sumsq.dtype != torch.float32 or not sumsq.is_contiguous():
+            raise ValueError('sumsq must be contiguous fp32 [tokens, hidden/64]')
+        target = None
+    else:
+        target = torch.empty_like(x) if out is None else out
+    nbytes = _lib.size_query("lm_moe_routes_combine_workspace_size", tokens, topk, hidden, inter, experts)
+    ws = (workspace or _SHARED).get(x.device, nbytes)
+    _lib.call("lm_moe_routes_combine_packed" if packed else "lm_moe_routes_combine", x.data_ptr(),
+              w1.data_ptr(), w2.data_ptr(), ids.data_ptr(), weights.data_ptr(), tokens, hidden, inter, experts,
+              topk, _lib.ptr(residual), float(alpha), _lib.ptr(sumsq if residual is not None else None),
+              _lib.ptr(target), ws.data_ptr(), ws.numel(), _lib.stream(x.device))
+    return sumsq if residual is not None else target
+
+
+def combine_supported(tokens, topk, hidden, inter):
+    """Whether :func:`moe_routes_combine` has kernels for this call."""
+    return (scan_path(tokens, topk) and topk <= 8 and hidden % 64 == 0 and hidden // 64 <= 256
+            and inter <= 1024 and hidden % 128 == 0 and inter % 128 == 0)
 
 
 def finish_add_rmsnorm(y, ids, scales, x, alpha, norm_weight, eps, z=None, logical=None):

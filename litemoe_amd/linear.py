@@ -51,6 +51,28 @@ def linear_splitk(a, weight, splits, out=None):
     return out
 
 
+def linear_splitk_rmsnorm(x, sumsq, norm_weight, eps, weight, splits, out=None):
+    """fp32 partials ``[splits, rows, out_features]`` of ``rmsnorm(x) @
+    weight.T``, the norm formed in the kernel from ``sumsq`` (the
+    per-64-column sums of squares of ``x`` that
+    :func:`experts.moe_routes_combine` writes): bitwise
+    ``linear_splitk(lm_rmsnorm(x), weight, splits)``."""
+    _lib.require_cuda(x, sumsq, norm_weight, weight, what="projection operands")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or norm_weight.dtype != torch.bfloat16:
+        raise ValueError("Split-K projection supports BF16 operands")
+    if x.dim() != 2 or not x.is_contiguous() or not weight.is_contiguous() or weight.shape[1] != x.shape[1]:
+        raise ValueError("Split-K projection needs a contiguous [rows, K] input and a contiguous [N, K] weight")
+    rows, k = x.shape
+    if sumsq.shape != (rows, k // 64) or sumsq.dtype != torch.float32 or not sumsq.is_contiguous():
+        raise ValueError("sumsq must be contiguous fp32 [rows, K/64]")
+    n = weight.shape[0]
+    if out is None:
+        out = torch.empty(splits, rows, n, device=x.device, dtype=torch.float32)
+    _lib.call("lm_linear_splitk_rmsnorm", x.data_ptr(), sumsq.data_ptr(), norm_weight.data_ptr(), float(eps),
+              weight.data_ptr(), rows, n, k, splits, out.data_ptr(), _lib.stream(x.device))
+    return out
+
+
 def frag_row_blocks(rows):
     """16-row blocks of the fragment order for ``rows`` rows: the smallest of
     1, 2, 4, 8 covering them (the split-K kernel's row-block count)."""

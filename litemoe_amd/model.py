@@ -33,9 +33,9 @@ import torch.nn.functional as F
 from . import _lib
 from .config import validate_config
 from .flash_decode import FlashDecode
-from .experts import finish_add_rmsnorm, pack_expert_weights, scan_path
-from .linear import linear_dense, linear_splitk, linear_splitk_frag, pick_splits
-from .norm import add_rmsnorm
+from .experts import combine_supported, finish_add_rmsnorm, pack_expert_weights, scan_path
+from .linear import linear_dense, linear_splitk, linear_splitk_frag, linear_splitk_rmsnorm, pick_splits
+from .norm import add_rmsnorm, rmsnorm
 from .packed import PackedPrefill, build_packed, varlen_attention
 from .rope import rope_kv_write
 from .router import add_rmsnorm_route as route_add_rmsnorm
@@ -62,6 +62,9 @@ class Granite:
         self.decode_flash = None   # FlashDecode set by the execution policy
         self.decode_lean = False   # positions pre-zeroed for stopped rows; outputs unmasked
         self.prefill_lean = False  # set by the optimized policy: batched prefill is packed
+        # decode option: the combine in the down projection, the next norm in
+        # the QKV projection (bitwise the same results; measured slower)
+        self.chain_combine = False
         self.used = None
         self._row_order = None     # the decode prologue's row order, during greedy_step only
         self.fused_head = True     # greedy_step: LM head with the argmax in its epilogue (lm_head_greedy)
@@ -151,7 +154,7 @@ class Granite:
         so = pick_splits(rows, cfg.hidden_size, cfg.num_attention_heads * d, max_splits=4)
         return (sq, so) if sq and so else None
 
-    def attention_splitk(self, z, w, cache, layer, rope_positions, active, splits):
+    def attention_splitk(self, z, w, cache, layer, rope_positions, active, splits, part=None):
         """Decode layer attention on the split-K projections: the packed QKV
         partials go to lm_flash_decode_qkv (reduction, RoPE, KV store and
         attention in one launch), and the o_proj partials are returned for
@@ -159,10 +162,13 @@ class Granite:
         output goes to o_proj in the split-K kernel's fragment order (1 KB
         per activation load; o_proj 5.48 -> 4.84 us at cfg 3). z stays
         row-major: its combine kernel writes whole rows, and the scattered
-        fragment-order stores there cost more than the QKV projection gains."""
+        fragment-order stores there cost more than the QKV projection gains.
+        ``part``: the QKV partials, when the caller formed them (e.g. with the
+        input norm fused in, :func:`linear_splitk_rmsnorm`)."""
         cfg = self.cfg
         rows = z.shape[0]
-        part = linear_splitk(z, w["self_attn.qkv_proj"], splits[0])
+        if part is None:
+            part = linear_splitk(z, w["self_attn.qkv_proj"], splits[0])
         flash = self._decode_attention(rows, cache)
         order = self._row_order if self._row_order is not None and self._row_order.shape[0] == rows else None
         a = flash.fused_qkv(part, self.cos_sin, rope_positions, active, cache.k[layer], cache.v[layer],
@@ -186,6 +192,8 @@ class Granite:
         layers = self.w["layers"]
         r, eps, k = cfg.residual_multiplier, cfg.rms_norm_eps, cfg.num_experts_per_tok
         splits = None if isinstance(slot, PackedPrefill) else self.decode_splits(x.shape[0])
+        if splits and self._combine_chain(x.shape[0]):
+            return self._chained_layers(x, z, cache, rope_positions, valid_rows, splits)
         for layer, w in enumerate(layers):
             if splits:
                 o_part = self.attention_splitk(z, w, cache, layer, rope_positions, valid_rows, splits)
@@ -205,6 +213,43 @@ class Granite:
             nxt = layers[layer + 1]["input_layernorm"] if layer + 1 < len(layers) else self.w["norm"]
             finish_add_rmsnorm(y, ids, weights, x, r, nxt, eps, z)
         return z
+
+    def _combine_chain(self, rows):
+        """Whether the decode layers run chained: the combine and the residual
+        add fused into the down projection (``lm_moe_routes_combine``) and
+        the next layer's input norm into its QKV projection
+        (``lm_linear_splitk_rmsnorm``). Off by default: at the 3B decode
+        shape the chained step measured 3.03-3.04 ms against 2.965-2.968 ms
+        (the last arriver's combine adds 2.6 us per layer at the end of the
+        down launch, forming the norm adds 1.6 us to the QKV projection,
+        against the 5.1 us combine launch they replace)."""
+        cfg = self.cfg
+        h, i = cfg.hidden_size, cfg.intermediate_size
+        return (self.chain_combine and self.pack_weights and "input_linear_packed" in self.w["layers"][0]
+                and h % 512 == 0 and h <= 2048 and combine_supported(rows, cfg.num_experts_per_tok, h, i))
+
+    def _chained_layers(self, x, z, cache, rope_positions, valid_rows, splits):
+        """The decode layers with four launches between attentions instead of
+        five: per layer the QKV projection (layer 0 from the prologue's z,
+        then with the input norm formed from ``x`` and the previous layer's
+        sums of squares), the attention, o_proj, add+norm+router (each
+        token's experts in id order), gate/up, and down with the combine and
+        the residual add. Bitwise the same x, z, KV cache and logits as the
+        unchained layers; the final norm is one lm_rmsnorm."""
+        cfg = self.cfg
+        r, eps, k = cfg.residual_multiplier, cfg.rms_norm_eps, cfg.num_experts_per_tok
+        sumsq = None
+        for layer, w in enumerate(self.w["layers"]):
+            part = None
+            if layer:
+                part = linear_splitk_rmsnorm(x, sumsq, w["input_layernorm"], eps, w["self_attn.qkv_proj"],
+                                             splits[0])
+            o_part = self.attention_splitk(z, w, cache, layer, rope_positions, valid_rows, splits, part=part)
+            weights, ids, z = route_add_rmsnorm_splitk(x, o_part, r, w["post_attention_layernorm"], eps,
+                                                       w["block_sparse_moe.router.layer"], k, z, id_order=True)
+            sumsq = self.ep.backend.routes_combine(z, w["input_linear_packed"], w["output_linear_packed"], ids,
+                                                   weights, residual=x, alpha=r, sumsq=sumsq, packed=True)
+        return rmsnorm(x, self.w["norm"], eps, out=z)
 
     def greedy_supported(self):
         """Whether :meth:`greedy_step` applies: lean decode on the fused tail,

@@ -34,9 +34,11 @@ def fused_topk(hidden_states, gating_output, topk, renormalize=True):
     return weights, ids, indices
 
 
-def route(z, gate_weight, topk, renormalize=True, logits_out=None):
+def route(z, gate_weight, topk, renormalize=True, logits_out=None, id_order=False):
     """Fused ``logits = bf16(z . W_r^T)`` then ``fused_topk``; ``z [M, H]``,
-    ``gate_weight [E, H]``. Optionally writes the bf16 logits."""
+    ``gate_weight [E, H]``. Optionally writes the bf16 logits. ``id_order``:
+    each token's experts (and weights) in ascending id instead of descending
+    logit."""
     _lib.require_cuda(z, gate_weight, what="router inputs")
     if z.dtype != torch.bfloat16 or gate_weight.dtype != torch.bfloat16:
         raise ValueError('Router supports BF16')
@@ -48,8 +50,8 @@ def route(z, gate_weight, topk, renormalize=True, logits_out=None):
     if logits_out is not None and (logits_out.shape != (m, experts) or logits_out.dtype != torch.bfloat16):
         raise ValueError('logits_out must be BF16 [tokens, experts]')
     _lib.call("lm_router", z.data_ptr(), gate_weight.data_ptr(), m, hidden, experts, topk,
-              int(bool(renormalize)), _lib.ptr(logits_out), weights.data_ptr(), ids.data_ptr(),
-              _lib.stream(z.device))
+              int(bool(renormalize)) | (2 if id_order else 0), _lib.ptr(logits_out), weights.data_ptr(),
+              ids.data_ptr(), _lib.stream(z.device))
     return weights, ids
 
 
@@ -74,10 +76,12 @@ def add_rmsnorm_route(x, a, alpha, norm_weight, eps, gate_weight, topk, z=None, 
 
 
 def add_rmsnorm_route_splitk(x, partials, alpha, norm_weight, eps, gate_weight, topk, z=None,
-                             renormalize=True, logits_out=None):
+                             renormalize=True, logits_out=None, id_order=False):
     """:func:`add_rmsnorm_route` with the residual branch given as split-K
     partials ``[S, M, H]`` of the attention output projection
-    (``a = bf16(sum of slices)``, litemoe/model.py:73 then :108-113)."""
+    (``a = bf16(sum of slices)``, litemoe/model.py:73 then :108-113).
+    ``id_order``: each token's experts (and weights) in ascending id, the
+    order :func:`experts.moe_routes_combine` sums in."""
     _lib.require_cuda(x, partials, norm_weight, gate_weight, what="router inputs")
     if x.dtype != torch.bfloat16 or not x.is_contiguous() or gate_weight.shape[1] != x.shape[-1]:
         raise ValueError('Router needs a contiguous BF16 [M, H] residual and [E, H] weight')
@@ -89,6 +93,7 @@ def add_rmsnorm_route_splitk(x, partials, alpha, norm_weight, eps, gate_weight, 
     weights, ids = _outputs(m, topk, x.device)
     _lib.call("lm_add_rmsnorm_router_splitk", x.data_ptr(), partials.data_ptr(), partials.shape[0],
               float(alpha), norm_weight.data_ptr(), float(eps), z.data_ptr(), gate_weight.data_ptr(), m,
-              hidden, experts, topk, int(bool(renormalize)), _lib.ptr(logits_out), weights.data_ptr(),
+              hidden, experts, topk, int(bool(renormalize)) | (2 if id_order else 0), _lib.ptr(logits_out),
+              weights.data_ptr(),
               ids.data_ptr(), _lib.stream(x.device))
     return weights, ids, z
