@@ -306,3 +306,24 @@ def test_varlen_attention_matches_sdpa_per_sequence():
             q[l:r].transpose(0, 1), k[l:r].transpose(0, 1).repeat_interleave(2, 0),
             v[l:r].transpose(0, 1).repeat_interleave(2, 0), is_causal=True, scale=0.125).transpose(0, 1))
     torch.testing.assert_close(got, torch.cat(parts), atol=1e-5, rtol=1e-5)
+
+
+def test_varlen_attention_non_causal_and_empty_sequence_match_sdpa():
+    """The non-causal branch (every token of a sequence attends every key of
+    it) against SDPA without a mask, per sequence, with an empty sequence
+    inside the pack and three q heads per kv head."""
+    torch.manual_seed(12)
+    q = torch.randn(12, 6, 64)
+    k, v = torch.randn(12, 2, 64), torch.randn(12, 2, 64)
+    cu = torch.tensor([0, 5, 5, 12])
+    got = ops.varlen_attention(q, k, v, cu, 0.125, causal=False)
+    parts = []
+    for l, r in [(0, 5), (5, 12)]:
+        parts.append(F.scaled_dot_product_attention(
+            q[l:r].transpose(0, 1), k[l:r].transpose(0, 1).repeat_interleave(3, 0),
+            v[l:r].transpose(0, 1).repeat_interleave(3, 0), is_causal=False, scale=0.125).transpose(0, 1))
+    torch.testing.assert_close(got, torch.cat(parts), atol=1e-5, rtol=1e-5)
+    # the causal and non-causal results agree on each sequence's last token only
+    causal = ops.varlen_attention(q, k, v, cu, 0.125)
+    torch.testing.assert_close(causal[[4, 11]], got[[4, 11]], atol=1e-6, rtol=1e-6)
+    assert not torch.allclose(causal[[0, 5]], got[[0, 5]])
