@@ -276,6 +276,20 @@ def prefill_bench(args):
             times.append(time.perf_counter() - t)
         elapsed = min(times[1:])
         log(f"prefill of {tokens} tokens: {elapsed * 1e3:.1f} ms")
+        # The same prefill with RoPE and the KV store as their own pass after
+        # the QKV projection (Granite.qkv_epilogue off).
+        model.qkv_epilogue = False
+        times = []
+        for _ in range(3):
+            engine.reset()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            engine.prefill()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t)
+        model.qkv_epilogue = True
+        unfused_ms = min(times[1:]) * 1e3
+        log(f"prefill, separate RoPE/KV pass: {unfused_ms:.1f} ms")
 
         # The MoE and the attention of one layer at the same token counts.
         H, I, E, k = cfg.hidden_size, cfg.intermediate_size, cfg.num_local_experts, cfg.num_experts_per_tok
@@ -315,12 +329,31 @@ def prefill_bench(args):
             projections[name] = {"ms": round(own, 4), "frac": round(flops / own / 1e9 / BF16_PEAK_TFLOPS, 4),
                                  "hipblaslt_ms": round(blas, 4),
                                  "hipblaslt_frac": round(flops / blas / 1e9 / BF16_PEAK_TFLOPS, 4)}
+        # QKV projection with RoPE + KV store in its epilogue against the projection then lm_rope_kv_write
+        from litemoe_amd.linear import linear_rope_kv
+        from litemoe_amd.rope import rope_kv_write
+        wq = layer["self_attn.qkv_proj"]
+        pos = torch.cat([torch.arange(n) for n in lengths]).to(dev)
+        slots = torch.repeat_interleave(torch.arange(len(lengths)), torch.tensor(lengths)).to(dev)
+        act = torch.ones(tokens, dtype=torch.bool, device=dev)
+        qkv = torch.empty(tokens, wq.shape[0], device=dev, dtype=torch.bfloat16)
+
+        def two_pass():
+            linear_dense(z, wq, out=qkv)
+            rope_kv_write(qkv[:, :hq * d].view(tokens, hq, d), qkv[:, hq * d:(hq + hkv) * d].view(tokens, hkv, d),
+                          qkv[:, (hq + hkv) * d:].view(tokens, hkv, d), pos, act, model.cos_sin, engine.cache, 0,
+                          slots=slots, write_k=True)
+
+        fused = hip_time(lambda: linear_rope_kv(z, wq, hq, hkv, pos, act, model.cos_sin, engine.cache, 0, slots), 5)
+        separate = hip_time(two_pass, 5)
+        projections["qkv_rope_kv"] = {"ms": round(fused, 4), "two_pass_ms": round(separate, 4)}
     line = {
         "metric": "prefill tok/s, Granite-3B-shape bf16, cfg4 packed prefill", "value": round(tokens / elapsed, 1),
         "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
         "data": "synthetic: random-init bf16 weights (seed 0), prompt ids (seed 1), lengths U{64..2048} (seed 2)",
         "config": {"workload": f"cfg4 packed prefill: {args.model} shape, 48 prompts, {tokens} tokens",
                    "tokens": tokens, "ms": round(elapsed * 1e3, 2)},
+        "separate_rope_kv_ms": round(unfused_ms, 2),
         "moe_mfma": {"flops_per_layer": moe_flops, "peak_tflops": BF16_PEAK_TFLOPS, **moe},
         "projections_mfma": projections,
         "attention_mfma": {"flops_per_layer": attn_flops, "ms_per_layer": round(ms, 3),

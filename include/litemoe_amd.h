@@ -414,6 +414,27 @@ int lm_linear(const void *a, int64_t lda, const void *weight, int64_t ldw,
               int64_t rows, int64_t out_features, int64_t in_features,
               void *out, int64_t ldo, void *stream);
 
+/* The packed QKV projection with RoPE and the KV-cache store in its epilogue:
+ *   qkv = lm_linear(a, weight)       (weight [(q_heads + 2*kv_heads)*64, K])
+ *   then lm_rope_kv_write on qkv's q|k|v heads with write_k = 1
+ * in one launch: each output row's q and k heads are rotated in registers and
+ * written to qkv rotated, k and v are stored into k_cache / v_cache at
+ * (slots[r], h, positions[r]) under the lm_kv_write mask. qkv and the caches
+ * are bitwise those of the two-call sequence. Replaces litemoe/model.py:47-49
+ * (F.linear of the packed q|k|v weight), :58 or :63-64 (rotary_embedding)
+ * and :59 / :70 (cache.write -> kv_write.py:23-29). Head dim 64. qkv: bf16
+ * [rows, (q_heads + 2*kv_heads)*64], row stride ldo (a multiple of 4,
+ * 8-byte aligned); active and slots may be NULL (every row stores; slot =
+ * row); k_cache and v_cache both NULL store nothing. Otherwise as lm_linear
+ * and lm_rope_kv_write. */
+int lm_linear_rope_kv(const void *a, int64_t lda, const void *weight,
+                      int64_t rows, int64_t q_heads, int64_t kv_heads,
+                      int64_t in_features, void *qkv, int64_t ldo,
+                      const int64_t *positions, const uint8_t *active,
+                      const int64_t *slots, const void *cos_sin,
+                      int64_t table_len, void *k_cache, void *v_cache,
+                      int64_t capacity, int64_t cache_batch, void *stream);
+
 /* ------------------------------------------------------ fused decode ops -- */
 
 /* Residual add, RMSNorm and the router in one pass per token:

@@ -63,6 +63,8 @@ _SIGNATURES = {
     "lm_linear_splitk_reduce": [_v, _i64, _i64, _i64, _v, _i64, _v],
     "lm_linear_splitk_rmsnorm": [_v, _v, _v, _f32, _v, _i64, _i64, _i64, _i64, _v, _v],
     "lm_linear": [_v, _i64, _v, _i64, _i64, _i64, _i64, _v, _i64, _v],
+    "lm_linear_rope_kv": [_v, _i64, _v, _i64, _i64, _i64, _i64, _v, _i64, _v, _v, _v, _v, _i64, _v, _v, _i64,
+                          _i64, _v],
     "lm_flash_decode_qkv": [_v, _i64, _v, _i64, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64,
                             _f32, _i64, _i64, _v, _v, _i64, _v],
     "lm_flash_decode_qkv_frag": [_v, _i64, _v, _i64, _v, _v, _v, _v, _v, _v, _i64, _i64, _i64, _i64, _i64,

@@ -45,12 +45,33 @@ __device__ __forceinline__ int frag_offset(int row, int chunk) {
   return row * kRowBytes + ((chunk ^ (row & 7)) << 4);
 }
 
+// The packed QKV projection's epilogue (lm_linear_rope_kv): each 64-column
+// block is one head (q heads, then k, then v); q and k are rotated (neox,
+// the three roundings of rope_kv_kernel) and written back rotated, k and v
+// are stored into the KV cache layer under lm_kv_write's mask.
+struct RopeKV {
+  const int64_t *pos;      // [M] RoPE table row and cache position of each row
+  const int64_t *slots;    // [M] cache row of each row, or NULL (the row index)
+  const uint8_t *active;   // [M], or NULL: every row stores
+  const bf16 *cos_sin;     // [table_len, 64]: cos | sin halves
+  int64_t table_len;
+  bf16 *kc, *vc;           // [cache_batch, kv_heads, capacity, 64]
+  int64_t capacity, cache_batch;
+  int q_heads, kv_heads;
+};
+
+__device__ __forceinline__ void rotate3(float x1, float x2, float c, float s, float &o1, float &o2) {
+  o1 = round_bf16(round_bf16(x1 * c) - round_bf16(x2 * s));
+  o2 = round_bf16(round_bf16(x2 * c) + round_bf16(x1 * s));
+}
+
 // kVec: ldo and out allow 8-byte stores and N % 4 == 0 (else 2-byte stores).
-template <int kTM, int kTN, int kWM, int kWN, bool kVec>
+// kRope: the RopeKV epilogue (64-column wave blocks, kVec).
+template <int kTM, int kTN, int kWM, int kWN, bool kVec, bool kRope = false>
 __global__ void __launch_bounds__(64 * kWM * kWN)
 gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w, int64_t ldw,
             bf16 *__restrict__ out, int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n,
-            int xcd_remap) {
+            int xcd_remap, RopeKV rk) {
   constexpr int kWaves = kWM * kWN;
   constexpr int kWaveRows = kTM / kWM, kWaveCols = kTN / kWN;
   constexpr int kRB = kWaveRows / 16, kCB = kWaveCols / 16;
@@ -148,6 +169,50 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
 
   // Transposed C fragment: lane holds output row m0 + wr*kWaveRows + rb*16 +
   // lane%16 and its columns 4*(lane/16) .. +3 of each 16-column block.
+  if constexpr (kRope) {
+    static_assert(kWaveCols == 64 && kVec, "one head per wave column block");
+    // Channel 16*cb + 4*fk + i and its neox partner (+32) sit in the same
+    // lane, blocks cb and cb + 2.
+    const int head = (n0 + wc * kWaveCols) / 64;  // uniform per wave
+    const bool rot = head < rk.q_heads + rk.kv_heads, is_k = rot && head >= rk.q_heads;
+    const int kvh = rot ? head - rk.q_heads : head - rk.q_heads - rk.kv_heads;
+    bf16 *cache = is_k ? rk.kc : rk.vc;
+#pragma unroll
+    for (int rb2 = 0; rb2 < kRB; ++rb2) {
+      const int row = m0 + wr * kWaveRows + rb2 * 16 + fr;
+      if (row >= M || head >= rk.q_heads + 2 * rk.kv_heads) continue;
+      const int64_t p = rk.pos[row];
+      const int64_t slot = rk.slots ? rk.slots[row] : row;
+      const bool store = (is_k || !rot) && cache && (!rk.active || rk.active[row]) && p >= 0 &&
+                         p < rk.capacity && slot >= 0 && slot < rk.cache_batch;
+      float v[4][4];
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[cb][i] = round_bf16(acc[rb2][cb][i]);
+      if (rot && p >= 0 && p < rk.table_len) {
+        const bf16 *cs = rk.cos_sin + p * 64;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const uint2 cw = *reinterpret_cast<const uint2 *>(cs + cb * 16 + 4 * fk);
+          const uint2 sw = *reinterpret_cast<const uint2 *>(cs + 32 + cb * 16 + 4 * fk);
+          const float c[4] = {lo_f32(cw.x), hi_f32(cw.x), lo_f32(cw.y), hi_f32(cw.y)};
+          const float sn[4] = {lo_f32(sw.x), hi_f32(sw.x), lo_f32(sw.y), hi_f32(sw.y)};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) rotate3(v[cb][i], v[cb + 2][i], c[i], sn[i], v[cb][i], v[cb + 2][i]);
+        }
+      }
+      bf16 *o = out + (int64_t)row * ldo + n0 + wc * kWaveCols + 4 * fk;
+      bf16 *dst = store ? cache + ((slot * rk.kv_heads + kvh) * rk.capacity + p) * 64 + 4 * fk : nullptr;
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const uint2 word = make_uint2(pack_bf16(v[cb][0], v[cb][1]), pack_bf16(v[cb][2], v[cb][3]));
+        *reinterpret_cast<uint2 *>(o + cb * 16) = word;
+        if (store) *reinterpret_cast<uint2 *>(dst + cb * 16) = word;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int rb2 = 0; rb2 < kRB; ++rb2) {
     const int row = m0 + wr * kWaveRows + rb2 * 16 + fr;
@@ -171,21 +236,39 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
 
 template <int TM, int TN, int WM, int WN>
 int launch_gemm_cfg(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16 *out, int64_t ldo,
-                    int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+                    int64_t M, int64_t N, int64_t K, hipStream_t stream, const RopeKV *rope = nullptr) {
   const int64_t tiles_m = cdiv(M, TM), tiles_n = cdiv(N, TN);
   // With fewer row tiles than XCDs the remap would put every tile on a few
   // XCDs; the plain order spreads the column tiles instead.
   const bool remap = tiles_m >= kXcds;
   const int64_t blocks = (remap ? align_up(tiles_m, kXcds) : tiles_m) * tiles_n;
   const bool vec = N % 4 == 0 && ldo % 4 == 0 && ((uintptr_t)out & 7) == 0;
-  if (vec)
-    gemm_kernel<TM, TN, WM, WN, true><<<dim3((unsigned)blocks), 64 * WM * WN, 0, stream>>>(
-        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap);
-  else
-    gemm_kernel<TM, TN, WM, WN, false><<<dim3((unsigned)blocks), 64 * WM * WN, 0, stream>>>(
-        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap);
+  const dim3 grid((unsigned)blocks);
+  if (rope) {
+    if (!vec) return LM_EINVAL;
+    gemm_kernel<TM, TN, WM, WN, true, true><<<grid, 64 * WM * WN, 0, stream>>>(
+        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap, *rope);
+  } else if (vec) {
+    gemm_kernel<TM, TN, WM, WN, true><<<grid, 64 * WM * WN, 0, stream>>>(
+        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap, RopeKV{});
+  } else {
+    gemm_kernel<TM, TN, WM, WN, false><<<grid, 64 * WM * WN, 0, stream>>>(
+        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap, RopeKV{});
+  }
   LM_CHECK_LAUNCH();
   return LM_OK;
+}
+
+// Prefill-sized row counts take 256 x 256 tiles on 16 waves of 64 x 64 (four
+// waves per SIMD). On one box at the cfg 4 QKV shape (46,990 x 1536 x 2560):
+// 443 us against 509 us for 8 waves of 64 x 128 (two per SIMD), 539-587 us
+// for 128 x 256 / 256 x 128 on 16 waves; at the o_proj shape 280 against
+// 326 us. Fewer rows keep 128 x 128 tiles, whose grid spreads over more CUs.
+int launch_gemm_rope(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16 *out, int64_t ldo,
+                     int64_t M, int64_t N, int64_t K, hipStream_t stream, const RopeKV *rope) {
+  if (M >= 2048)
+    return launch_gemm_cfg<256, 256, 4, 4>(a, lda, w, ldw, out, ldo, M, N, K, stream, rope);
+  return launch_gemm_cfg<128, 128, 2, 2>(a, lda, w, ldw, out, ldo, M, N, K, stream, rope);
 }
 
 }  // namespace
@@ -197,21 +280,36 @@ bool gemm_shape_ok(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
          (N - 1) * ldw + K < lim && tiles < lim;
 }
 
-// Prefill-sized row counts take 256 x 256 tiles on 16 waves of 64 x 64 (four
-// waves per SIMD). On one box at the cfg 4 QKV shape (46,990 x 1536 x 2560):
-// 443 us against 509 us for 8 waves of 64 x 128 (two per SIMD), 539-587 us
-// for 128 x 256 / 256 x 128 on 16 waves; at the o_proj shape 280 against
-// 326 us. Fewer rows keep 128 x 128 tiles, whose grid spreads over more CUs.
 int launch_gemm(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16 *out, int64_t ldo,
                 int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-  if (M >= 2048)
-    return launch_gemm_cfg<256, 256, 4, 4>(a, lda, w, ldw, out, ldo, M, N, K, stream);
-  return launch_gemm_cfg<128, 128, 2, 2>(a, lda, w, ldw, out, ldo, M, N, K, stream);
+  return launch_gemm_rope(a, lda, w, ldw, out, ldo, M, N, K, stream, nullptr);
 }
 
 }  // namespace lm
 
 using namespace lm;
+
+extern "C" int lm_linear_rope_kv(const void *a, int64_t lda, const void *weight, int64_t rows,
+                                 int64_t q_heads, int64_t kv_heads, int64_t in_features, void *qkv,
+                                 int64_t ldo, const int64_t *positions, const uint8_t *active,
+                                 const int64_t *slots, const void *cos_sin, int64_t table_len,
+                                 void *k_cache, void *v_cache, int64_t capacity,
+                                 int64_t cache_batch, void *stream) {
+  const int64_t n = (q_heads + 2 * kv_heads) * 64;
+  LM_REQUIRE(rows >= 0 && q_heads > 0 && kv_heads > 0 && in_features > 0 && lda >= in_features &&
+             lda % 8 == 0 && ldo >= n && ldo % 4 == 0 && capacity >= 0 && cache_batch >= 0 &&
+             table_len >= 0);
+  if (rows == 0) return LM_OK;
+  if (!gemm_shape_ok(rows, n, in_features, lda, in_features)) return LM_EUNSUPPORTED;
+  LM_REQUIRE(a && weight && qkv && positions && cos_sin);
+  LM_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)weight & 15) == 0 && ((uintptr_t)qkv & 7) == 0 &&
+             ((uintptr_t)cos_sin & 7) == 0);
+  LM_REQUIRE((k_cache == nullptr) == (v_cache == nullptr));
+  const RopeKV rope{positions, slots, active, (const bf16 *)cos_sin, table_len, (bf16 *)k_cache,
+                    (bf16 *)v_cache, capacity, cache_batch, (int)q_heads, (int)kv_heads};
+  return launch_gemm_rope((const bf16 *)a, lda, (const bf16 *)weight, in_features, (bf16 *)qkv, ldo, rows,
+                          n, in_features, (hipStream_t)stream, &rope);
+}
 
 extern "C" int lm_linear(const void *a, int64_t lda, const void *weight, int64_t ldw, int64_t rows,
                          int64_t out_features, int64_t in_features, void *out, int64_t ldo,

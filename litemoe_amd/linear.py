@@ -181,3 +181,36 @@ def linear_dense(a, weight, out=None):
         _lib.call("lm_linear", a.data_ptr(), max(a.stride(0), k), weight.data_ptr(), max(weight.stride(0), k),
                   rows, n, k, out.data_ptr(), max(out.stride(0), n), _lib.stream(a.device))
     return out
+
+
+def linear_rope_kv(a, weight, q_heads, kv_heads, positions, active, cos_sin, cache, layer, slots=None):
+    """``linear_dense(a, weight)`` of the packed q|k|v weight followed by
+    ``rope_kv_write(q, k, v, ..., write_k=True)`` in one launch
+    (``lm_linear_rope_kv``): returns ``qkv [rows, (q_heads + 2*kv_heads)*64]``
+    with q and k rotated; k and v stored into ``cache`` layer ``layer`` at
+    ``(slots[r], h, positions[r])`` for active rows. Bitwise the two-call
+    result. Replaces litemoe/model.py:47-49 with :58-59 / :63-70."""
+    _lib.require_cuda(a, weight, cos_sin, positions, what="projection operands")
+    if a.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or cos_sin.dtype != torch.bfloat16:
+        raise ValueError("Fused QKV projection supports BF16 operands")
+    rows, k = a.shape
+    n = (q_heads + 2 * kv_heads) * 64
+    if weight.shape != (n, k) or not weight.is_contiguous() or k % 64:
+        raise ValueError("Fused QKV projection needs a contiguous [(q+2kv)*64, K] weight, K a multiple of 64")
+    if cos_sin.shape[-1] != 64 or not cos_sin.is_contiguous():
+        raise ValueError("Fused QKV projection needs a contiguous [table_len, 64] cos/sin table")
+    if rows and (a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16):
+        raise ValueError("Dense projection needs 16-byte aligned input rows with a stride a multiple of 8")
+    kc, vc = cache.k[layer], cache.v[layer]
+    if kc.dtype != torch.bfloat16 or kc.shape[1] != kv_heads or kc.shape[-1] != 64:
+        raise ValueError("Fused QKV projection needs a bf16 cache with head_dim 64")
+    out = torch.empty(rows, n, device=a.device, dtype=torch.bfloat16)
+    if rows:
+        positions = positions.to(torch.int64).contiguous()
+        active = None if active is None else active.to(torch.bool).contiguous()
+        slots = None if slots is None else slots.to(torch.int64).contiguous()
+        _lib.call("lm_linear_rope_kv", a.data_ptr(), max(a.stride(0), k), weight.data_ptr(), rows, q_heads,
+                  kv_heads, k, out.data_ptr(), n, positions.data_ptr(), _lib.ptr(active), _lib.ptr(slots),
+                  cos_sin.data_ptr(), cos_sin.shape[0], kc.data_ptr(), vc.data_ptr(), cache.capacity,
+                  kc.shape[0], _lib.stream(a.device))
+    return out

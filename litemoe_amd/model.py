@@ -34,7 +34,8 @@ from . import _lib
 from .config import validate_config
 from .flash_decode import FlashDecode
 from .experts import combine_supported, finish_add_rmsnorm, pack_expert_weights, scan_path
-from .linear import linear_dense, linear_splitk, linear_splitk_frag, linear_splitk_rmsnorm, pick_splits
+from .linear import (linear_dense, linear_rope_kv, linear_splitk, linear_splitk_frag, linear_splitk_rmsnorm,
+                     pick_splits)
 from .norm import add_rmsnorm, rmsnorm
 from .packed import PackedPrefill, build_packed, varlen_attention
 from .rope import rope_kv_write
@@ -65,6 +66,9 @@ class Granite:
         # decode option: the combine in the down projection, the next norm in
         # the QKV projection (bitwise the same results; measured slower)
         self.chain_combine = False
+        # attention(): RoPE and the KV store in the QKV projection's epilogue
+        # (lm_linear_rope_kv) rather than a separate lm_rope_kv_write pass
+        self.qkv_epilogue = True
         self.used = None
         self._row_order = None     # the decode prologue's row order, during greedy_step only
         self.fused_head = True     # greedy_step: LM head with the argmax in its epilogue (lm_head_greedy)
@@ -126,13 +130,19 @@ class Granite:
         rows = z.shape[0]
         d = cfg.hidden_size // cfg.num_attention_heads
         hq, hkv = cfg.num_attention_heads, cfg.num_key_value_heads
-        qkv = linear_dense(z, w["self_attn.qkv_proj"])
+        packed = isinstance(slot, PackedPrefill)
+        slots = slot.slots if packed else None
+        if self.qkv_epilogue:
+            qkv = linear_rope_kv(z, w["self_attn.qkv_proj"], hq, hkv, rope_positions, active, self.cos_sin,
+                                 cache, layer, slots)
+        else:
+            qkv = linear_dense(z, w["self_attn.qkv_proj"])
         q = qkv[:, :hq * d].view(rows, hq, d)
         k = qkv[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
         v = qkv[:, (hq + hkv) * d:].view(rows, hkv, d)
-        packed = isinstance(slot, PackedPrefill)
-        rope_kv_write(q, k, v, rope_positions, active, self.cos_sin, cache, layer,
-                      slots=slot.slots if packed else None, write_k=packed)
+        if not self.qkv_epilogue:
+            rope_kv_write(q, k, v, rope_positions, active, self.cos_sin, cache, layer, slots=slots,
+                          write_k=packed)
         if packed:
             a = varlen_attention(q, k, v, slot.cu, slot.maximum, cfg.attention_multiplier)
         else:

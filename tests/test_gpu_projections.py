@@ -150,6 +150,56 @@ def test_linear_dense_rejections():
     assert linear.linear_dense(bf((0, 128)).to(DEV), bf((32, 128)).to(DEV)).shape == (0, 32)
 
 
+class _Cache:
+    def __init__(self, layers, batch, hkv, cap):
+        self.capacity = cap
+        shape = (layers, batch, hkv, cap, 64)
+        self.k = torch.full(shape, 7.0, device=DEV, dtype=torch.bfloat16)
+        self.v = torch.full(shape, -3.0, device=DEV, dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,hq,hkv,k,batch,cap,table,masked", [
+    (5000, 24, 8, 1536, 6, 1024, 1024, False),   # cfg 3/4 layer shape, 256 x 256 tiles
+    (3001, 16, 8, 1024, 4, 1024, 900, True),     # cfg 2 shape; positions past the table
+    (700, 24, 8, 1536, 3, 512, 512, True),       # 128 x 128 tiles
+    (37, 8, 4, 512, 2, 64, 64, False), (1, 24, 8, 1536, 1, 16, 16, False)])
+@torch.inference_mode()
+def test_linear_rope_kv_equals_projection_then_rope_kv_write(rows, hq, hkv, k, batch, cap, table, masked):
+    """lm_linear_rope_kv against lm_linear then lm_rope_kv_write(write_k=1):
+    the rotated qkv and both cache layers bit for bit, with packed-prefill
+    slots and positions, inactive rows, rows whose position or slot is out
+    of range (not stored) and positions past the RoPE table (not rotated)."""
+    g = torch.Generator(device=DEV).manual_seed(rows + k)
+    a = torch.randn(rows, k, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.randn((hq + 2 * hkv) * 64, k, generator=g, device=DEV) * 0.03).to(torch.bfloat16)
+    cos_sin, _, _ = ops.rope_tables(1e4, 64, table, torch.bfloat16)
+    cos_sin = cos_sin.to(DEV)
+    # distinct (slot, position) pairs: one writer per cache entry
+    cell = torch.randperm(batch * cap, generator=g, device=DEV)[:rows]
+    slots, pos = cell // cap, cell % cap
+    active = torch.ones(rows, dtype=torch.bool, device=DEV)
+    if masked:
+        active = torch.rand(rows, generator=g, device=DEV) > 0.2
+        pos[::7] = cap + 3          # past capacity (and past the table)
+        pos[::11] = -1
+        slots[::13] = batch         # past the cache batch
+    layer = 1
+    ref_cache, got_cache = _Cache(3, batch, hkv, cap), _Cache(3, batch, hkv, cap)
+    ref = linear.linear_dense(a, w)
+    q = ref[:, :hq * 64].view(rows, hq, 64)
+    kk = ref[:, hq * 64:(hq + hkv) * 64].view(rows, hkv, 64)
+    v = ref[:, (hq + hkv) * 64:].view(rows, hkv, 64)
+    rope.rope_kv_write(q, kk, v, pos, active, cos_sin, ref_cache, layer, slots=slots, write_k=True)
+    for rep in range(2):
+        got = linear.linear_rope_kv(a, w, hq, hkv, pos, None if not masked and rep else active, cos_sin,
+                                    got_cache, layer, slots)
+        assert torch.equal(got, ref), rep
+        assert torch.equal(got_cache.k, ref_cache.k) and torch.equal(got_cache.v, ref_cache.v), rep
+    # a row range alone: the same rows
+    got = linear.linear_rope_kv(a[:3], w, hq, hkv, pos[:3], None, cos_sin, got_cache, layer, slots[:3])
+    assert torch.equal(got, ref[:3])
+
+
 def _qkv_case(b, hq, hkv, cap, splits, seed):
     g = torch.Generator().manual_seed(seed)
     ncols = (hq + 2 * hkv) * 64
