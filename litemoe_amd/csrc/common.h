@@ -117,6 +117,23 @@ __device__ __forceinline__ float dpp_sum8(float v) {
   return v;
 }
 
+// Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4):
+// lane l's bytes at base + voff land at LDS byte lds + 16 * l (lds in M0,
+// wave-uniform; base wave-uniform). Written as asm so that the compiler's
+// wait-count pass does not take it for a load that every later LDS read must
+// wait for (it cannot tell which LDS bytes the copy writes); the caller waits
+// with lds_copy_wait() and then a barrier before the bytes are read.
+__device__ __forceinline__ void lds_copy16(const void *base, uint32_t voff, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+}
+// Wait until every vector memory operation this wave issued has completed
+// (s_waitcnt vmcnt(0)), LDS copies included.
+__device__ __forceinline__ void lds_copy_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// The 32-bit LDS address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char *)p;
+}
+
 // acc + the dot product of the eight bf16 values of two 16-byte words: four
 // v_dot2_f32_bf16 in channel-pair order (each adds two exact bf16 products).
 // The pairs are taken with shufflevector from a bf16x8 view: bit-casting the

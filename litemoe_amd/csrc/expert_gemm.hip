@@ -60,7 +60,10 @@ template <int TM, int TN, int WMv, int WNv, int StagesV>
 struct TileCfg {
   static constexpr int M = TM, N = TN, WM = WMv, WN = WNv, Stages = StagesV;
 };
-using LargeTile = TileCfg<256, 256, 4, 2, 2>;
+#ifndef LM_EXPERT_LARGE_WN
+#define LM_EXPERT_LARGE_WN 2
+#endif
+using LargeTile = TileCfg<256, 256, 4, LM_EXPERT_LARGE_WN, 2>;
 using SmallTile = TileCfg<128, 128, 2, 2, 1>;
 constexpr int64_t kLargeTileRoutesPerExpert = 1024;
 
@@ -126,7 +129,10 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   static_assert(kLA * 8 * kWaves == kTM && kLB * 8 * kWaves == kTN, "tile rows per load round");
   static_assert(!kGateUp || kCB % 2 == 0, "gate/up waves hold gate and up blocks in pairs");
   constexpr int kABytes = kTM * kRowBytes, kStageBytes = (kTM + kTN) * kRowBytes;
-  __shared__ __align__(16) char smem[kStages * kStageBytes];
+  // kStages == 2: two LDS stages filled by direct copies; kStages == 1: one,
+  // filled from registers.
+  __shared__ __align__(16) char smem[kStageBytes];
+  __shared__ __align__(16) char smem1[kStages == 2 ? kStageBytes : 16];
   __shared__ int route_of[kTM];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   // Workgroups are dealt to the 8 XCDs round-robin in launch order. Remap so
@@ -169,9 +175,8 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   }
   // element advance of one kBK step of B (two 32-wide k-steps when packed)
   constexpr int kBStep = kPacked ? (int)(kBK / 32 * wstep<true>()) : kBK;
-  // One register stage: step k+1 is loaded while step k is computed from
-  // LDS, then stored to the other LDS buffer (two stages) or to the same one
-  // after a barrier (one stage).
+  // One stage: step k+1 is loaded into registers while step k is computed
+  // from LDS, then stored to LDS after a barrier.
   u32x4 ra[kLA], rbv[kLB];
   auto load = [&](int kt) {
     const int k0 = kt * kBK;
@@ -180,13 +185,25 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
 #pragma unroll
     for (int i = 0; i < kLB; ++i) rbv[i] = *reinterpret_cast<const u32x4 *>(w + ob[i] + kt * kBStep);
   };
-  auto store = [&](int buf) {
-    char *base = smem + buf * kStageBytes + lane * 16;
+  auto store = [&]() {
+    char *base = smem + lane * 16;
 #pragma unroll
     for (int i = 0; i < kLA; ++i) *reinterpret_cast<u32x4 *>(base + (wave * kLA + i) * 1024) = ra[i];
 #pragma unroll
     for (int i = 0; i < kLB; ++i)
       *reinterpret_cast<u32x4 *>(base + kABytes + (wave * kLB + i) * 1024) = rbv[i];
+  };
+  // Two stages: step k+1 is copied from global memory straight into the
+  // other stage while step k is computed (byte offsets: the element offsets
+  // are below 2^31).
+  const uint32_t uw = __builtin_amdgcn_readfirstlane(wave);
+  auto issue = [&](int kt, const char *stage) {
+    const bf16 *ak = a_src + kt * kBK, *wk = w + kt * kBStep;
+    const uint32_t la = lds_address(stage) + uw * kLA * 1024, lb = lds_address(stage) + kABytes + uw * kLB * 1024;
+#pragma unroll
+    for (int i = 0; i < kLA; ++i) lds_copy16(ak, (uint32_t)oa[i] * 2, la + i * 1024);
+#pragma unroll
+    for (int i = 0; i < kLB; ++i) lds_copy16(wk, (uint32_t)ob[i] * 2, lb + i * 1024);
   };
 
   const int wr = wave / kWN, wc = wave % kWN;
@@ -204,8 +221,7 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
 #pragma unroll
     for (int jj = 0; jj < kCB; ++jj) acc[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int buf) {
-    const char *as = smem + buf * kStageBytes;
+  auto compute = [&](const char *as) {
     const char *bs = as + kABytes;
 #pragma unroll
     for (int kk = 0; kk < kBK / 32; ++kk) {
@@ -227,23 +243,39 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   };
 
   const int nk = K / kBK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt + 1 < nk; ++kt) {
-    load(kt + 1);
-    __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
-    if constexpr (kStages == 2) {
-      compute(kt & 1);
-      store((kt + 1) & 1);  // the buffer no wave reads in this step
-    } else {
-      compute(0);
-      __syncthreads();  // every wave is done with the buffer
-      store(0);
+  if constexpr (kStages == 2) {
+    // Before a stage is read: this wave's copies have landed (vmcnt) and the
+    // barrier has seen every wave's, and every wave has left the step that
+    // last read the stage the next copy goes into.
+    issue(0, smem);
+    for (int kt = 0; kt < nk; kt += 2) {
+      lds_copy_wait();
+      __syncthreads();
+      if (kt + 1 < nk) issue(kt + 1, smem1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(smem);
+      if (kt + 1 < nk) {
+        lds_copy_wait();
+        __syncthreads();
+        if (kt + 2 < nk) issue(kt + 2, smem);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(smem1);
+      }
     }
+  } else {
+    load(0);
+    store();
     __syncthreads();
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      load(kt + 1);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
+      compute(smem);
+      __syncthreads();  // every wave is done with the buffer
+      store();
+      __syncthreads();
+    }
+    compute(smem);
   }
-  compute(kStages == 2 ? (nk - 1) & 1 : 0);
 
   // Transposed C fragment: lane holds output row lane%16 of each 16-row block
   // and its output columns 4*(lane/16) .. +3 of each 16-column block, written

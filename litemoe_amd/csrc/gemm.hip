@@ -16,12 +16,14 @@
 // Workgroup = kTM x kTN output tile (256 x 256 on 16 waves, or 128 x 128 on
 // 4), kWM x kWN waves, each wave a (kTM/kWM) x (kTN/kWN) block of 16 x 16
 // MFMA tiles; K runs in steps of 64.
-// The next step's A and B rows are loaded into registers while the MFMAs run
-// on the current step's LDS tile, then stored into the other of two LDS
-// buffers (one barrier per step). An LDS row is 64 bf16 = 8 chunks of 16
-// bytes; chunk c of tile row r sits at position c ^ (r & 7), so the 16 rows of
-// one fragment read spread over the banks and each wave's stores fill 1 KB
-// contiguously. The weights are the MFMA's first operand, so a lane ends with
+// The next step's A and B rows are copied from global memory straight into
+// the other of two LDS stages (global_load_lds_dwordx4, no register staging)
+// while the MFMAs run on the current step's stage; one barrier per step. An
+// LDS row is 64 bf16 = 8 chunks of 16 bytes; chunk c of tile row r sits at
+// position c ^ (r & 7), so the 16 rows of one fragment read spread over the
+// banks, and each copy instruction fills 1 KB contiguously. At the cfg 4 QKV
+// shape (46,990 x 1536 -> 2560, one box) the copies take the projection from
+// 472 to 365 us against register staging; at the o_proj shape 261 -> 220 us. The weights are the MFMA's first operand, so a lane ends with
 // four consecutive output columns of one row and stores them as one 8-byte
 // word.
 //
@@ -78,7 +80,8 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
   constexpr int kLA = kTM / (8 * kWaves), kLB = kTN / (8 * kWaves);  // 16-byte loads per lane
   static_assert(kLA * 8 * kWaves == kTM && kLB * 8 * kWaves == kTN, "tile rows per load round");
   constexpr int kABytes = kTM * kRowBytes, kStage = (kTM + kTN) * kRowBytes;
-  __shared__ __align__(16) char smem[2 * kStage];
+  __shared__ __align__(16) char s0[kStage];  // two LDS stages
+  __shared__ __align__(16) char s1[kStage];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int lin = blockIdx.x;
   int tile_m = lin / tiles_n, tile_n = lin % tiles_n;
@@ -91,38 +94,33 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
   if (tile_m >= tiles_m) return;
   const int m0 = tile_m * kTM, n0 = tile_n * kTN;
 
-  // Load instruction i of wave w fills LDS rows 8*(w*L+i) .. +7 (1 KB):
-  // lane l writes row 8*(w*L+i) + l/8 at position l%8, holding chunk
-  // (l%8) ^ (l/8), which is frag_offset's swizzle. Rows past M or N repeat
-  // the last row (finite values; their outputs are not stored).
-  // 32-bit element offsets (the host checks that every row start fits).
+  // Copy instruction i of wave w fills LDS rows 8*(w*L+i) .. +7 of an
+  // operand (1 KB; lane l at byte 16*l): row 8*(w*L+i) + l/8, position l%8,
+  // holding chunk (l%8) ^ (l/8), which is frag_offset's swizzle. Rows past M
+  // or N repeat the last row (finite values; their outputs are not stored).
+  // Byte offsets from the k step's base fit 32 bits (the host checks that
+  // every row start's element offset is below 2^31).
   const int chunk = (lane & 7) ^ (lane >> 3);
   uint32_t oa[kLA], ob[kLB];
 #pragma unroll
   for (int i = 0; i < kLA; ++i) {
     const int r = min(m0 + 8 * (wave * kLA + i) + lane / 8, M - 1);
-    oa[i] = (uint32_t)r * (uint32_t)lda + chunk * 8;
+    oa[i] = ((uint32_t)r * (uint32_t)lda + chunk * 8) * 2;
   }
 #pragma unroll
   for (int i = 0; i < kLB; ++i) {
     const int r = min(n0 + 8 * (wave * kLB + i) + lane / 8, N - 1);
-    ob[i] = (uint32_t)r * (uint32_t)ldw + chunk * 8;
+    ob[i] = ((uint32_t)r * (uint32_t)ldw + chunk * 8) * 2;
   }
-  u32x4 ra[kLA], rb[kLB];
-  auto load = [&](int kt) {
-    const uint32_t k0 = kt * kBK;
+  const uint32_t uw = __builtin_amdgcn_readfirstlane(wave);
+  // Step kt's A and B rows straight into an LDS stage (no register staging).
+  auto issue = [&](int kt, const char *stage) {
+    const bf16 *ak = a + kt * kBK, *wk = w + kt * kBK;
+    const uint32_t la = lds_address(stage) + uw * kLA * 1024, lb = lds_address(stage) + kABytes + uw * kLB * 1024;
 #pragma unroll
-    for (int i = 0; i < kLA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a + (oa[i] + k0));
+    for (int i = 0; i < kLA; ++i) lds_copy16(ak, oa[i], la + i * 1024);
 #pragma unroll
-    for (int i = 0; i < kLB; ++i) rb[i] = *reinterpret_cast<const u32x4 *>(w + (ob[i] + k0));
-  };
-  auto store = [&](int buf) {
-    char *base = smem + buf * kStage + lane * 16;
-#pragma unroll
-    for (int i = 0; i < kLA; ++i) *reinterpret_cast<u32x4 *>(base + (wave * kLA + i) * 1024) = ra[i];
-#pragma unroll
-    for (int i = 0; i < kLB; ++i)
-      *reinterpret_cast<u32x4 *>(base + kABytes + (wave * kLB + i) * 1024) = rb[i];
+    for (int i = 0; i < kLB; ++i) lds_copy16(wk, ob[i], lb + i * 1024);
   };
 
   const int wr = wave / kWN, wc = wave % kWN;
@@ -133,8 +131,7 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
 #pragma unroll
     for (int jj = 0; jj < kCB; ++jj) acc[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int buf) {
-    const char *as = smem + buf * kStage;
+  auto compute = [&](const char *as) {
     const char *bs = as + kABytes;
 #pragma unroll
     for (int kk = 0; kk < kBK / 32; ++kk) {
@@ -152,19 +149,25 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
     }
   };
 
+  // Step kt + 1 is copied into the other stage while step kt is computed.
+  // Before a stage is read: this wave's copies have landed (vmcnt) and the
+  // barrier has seen every wave's, and every wave has left the step that
+  // last read the stage the next copy goes into.
   const int nk = K / kBK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) load(kt + 1);
-    __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
-    compute(kt & 1);
-    // The other buffer was last read in step kt - 1, which every wave has
-    // left (the barrier below closed it).
-    if (more) store((kt + 1) & 1);
+  issue(0, s0);
+  for (int kt = 0; kt < nk; kt += 2) {
+    lds_copy_wait();
     __syncthreads();
+    if (kt + 1 < nk) issue(kt + 1, s1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(s0);
+    if (kt + 1 < nk) {
+      lds_copy_wait();
+      __syncthreads();
+      if (kt + 2 < nk) issue(kt + 2, s0);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(s1);
+    }
   }
 
   // Transposed C fragment: lane holds output row m0 + wr*kWaveRows + rb*16 +
