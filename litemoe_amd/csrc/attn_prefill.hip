@@ -1,9 +1,9 @@
 // Packed variable-length (causal) attention on MFMA, head_dim 64.
 //
 // Workgroup (query block of 128, q head, sequence); wave w owns two 16-query
-// sub-blocks. Keys stream in tiles of 64 staged through LDS, K and V both
-// row-major; the next tile is loaded into registers while the current one is
-// computed.
+// sub-blocks. Keys stream in tiles of 64 through two LDS stages, K and V both
+// row-major, copied straight from global memory (global_load_lds_dwordx4)
+// into one stage while the other is computed.
 // Scores are computed transposed, S^T = K . Q^T, so each lane's C fragment
 // (keys 16h + 4*(l/16) + i, query l%16) is directly the A operand of P . V:
 // the eight keys a lane holds become the eight k slots of one
@@ -28,8 +28,7 @@ namespace {
 constexpr int kD = 64;
 constexpr int kThreads = 256;
 constexpr int kBK = 64;
-constexpr int kStage = kBK / 32;  // keys each staging thread loads per tile (one per 32)
-constexpr int kKPad = 8;
+constexpr int kRowBytes = kD * 2;  // one key row in LDS (no padding: rows are XOR-swizzled)
 constexpr float kLazy = 8.f;
 constexpr uint32_t kOnes = 0x3F803F80u;  // two bf16 1.0
 
@@ -55,19 +54,23 @@ __device__ __forceinline__ uint2 read_tr(const bf16 *p) {
 // Per query the arithmetic is the same for every kQS (a tile that is fully
 // masked for one sub-block adds exact zeros to its state).
 template <int kQS>
-// Four waves per SIMD (<= 128 registers; the Q fragments live in LDS for it):
-// 0.350 -> 0.328 ms per layer at cfg 4 against three waves with Q in registers.
+// Four waves per SIMD (<= 128 registers). With the K/V tiles staged through
+// registers the Q fragments had to live in LDS to fit (0.350 -> 0.328 ms per
+// layer at cfg 4 against three waves); the direct copies free those
+// registers, so Q is back in registers, and the second LDS stage takes Q's
+// LDS: 0.311 -> 0.282 ms per layer at cfg 4.
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
 prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 *__restrict__ k,
                int64_t ks0, int64_t ks1, const bf16 *__restrict__ v, int64_t vs0, int64_t vs1,
                const int32_t *__restrict__ cu, int q_heads, int kv_heads, float scale, int causal,
                bf16 *__restrict__ out) {
   constexpr int kBQ = 64 * kQS;
-  __shared__ __attribute__((aligned(16))) bf16 ks_lds[kBK][kD + kKPad];
-  __shared__ __attribute__((aligned(16))) bf16 vs_lds[kBK][kD + kKPad];
-  // the workgroup's Q fragments, lane-major (re-read each tile instead of
-  // held in 16 registers: four waves per SIMD fit in 128 registers)
-  __shared__ __attribute__((aligned(16))) u32x4 qs_lds[4][kQS][2][kWave];
+  // Two stages of one key tile each: K rows (64 x 128 bytes) then V rows,
+  // filled by direct global -> LDS copies. 16-byte chunk c of K row r sits at
+  // c ^ (r & 7) (the 8 rows of a fragment read hit 8 different bank groups);
+  // of V row r at c ^ 2(r & 3) (the 4 rows of one transposing read group hit
+  // 4 different 32-byte bank groups).
+  __shared__ __attribute__((aligned(16))) char kv_lds[2][2 * kBK * kRowBytes];
   const int qb = blockIdx.x, hq = blockIdx.y, seq = blockIdx.z;
   const int start = cu[seq];
   const int len = cu[seq + 1] - start;
@@ -80,20 +83,20 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
   const float sl2 = scale * 1.4426950408889634f;
 
   // Sub-block qs: queries wq0 + 16 qs + (0..15); lane col owns query
-  // wq0 + 16 qs + col's softmax state.
+  // wq0 + 16 qs + col's softmax state and holds its Q fragments.
   float m[kQS];
   f32x4 o[kQS][4], lsum[kQS];  // lsum: C layout of o, every column the row sum
+  u32x4 qf0[kQS], qf1[kQS];
 #pragma unroll
   for (int qs = 0; qs < kQS; ++qs) {
     const int qi = wq0 + 16 * qs + col;
-    u32x4 f0 = u32x4{0u, 0u, 0u, 0u}, f1 = f0;
+    qf0[qs] = u32x4{0u, 0u, 0u, 0u};
+    qf1[qs] = qf0[qs];
     if (qi < len) {
       const bf16 *qp = q + (int64_t)(start + qi) * qs0 + (int64_t)hq * qs1 + grp * 8;
-      f0 = *reinterpret_cast<const u32x4 *>(qp);
-      f1 = *reinterpret_cast<const u32x4 *>(qp + 32);
+      qf0[qs] = *reinterpret_cast<const u32x4 *>(qp);
+      qf1[qs] = *reinterpret_cast<const u32x4 *>(qp + 32);
     }
-    qs_lds[wave][qs][0][lane] = f0;  // read back by the same lane only
-    qs_lds[wave][qs][1][lane] = f1;
     m[qs] = -INFINITY;
     lsum[qs] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -102,48 +105,49 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
 
   const int kend = causal ? min(len, q0 + kBQ) : len;
   const bool wave_live = wq0 < len;
-  // Tile staging: thread -> (key skey, channels 8*sdc..+7). Keys past the
-  // sequence repeat its last key (finite values; their scores are masked).
-  const int skey = threadIdx.x / 8, sdc = threadIdx.x % 8;
-  const bf16 *kbase = k + (int64_t)start * ks0 + (int64_t)hk * ks1 + sdc * 8;
-  const bf16 *vbase = v + (int64_t)start * vs0 + (int64_t)hk * vs1 + sdc * 8;
-  auto load = [&](int kt, u32x4 *kv, u32x4 *vv) {
+  // Copy instruction i of wave w fills LDS rows 8*(2w+i) .. +7 of the K (V)
+  // tile: lane l writes row 8*(2w+i) + l/8 at position l%8, so it fetches
+  // the chunk that position holds. Keys past the sequence repeat its last
+  // key (finite values; their scores are masked). Byte offsets from the
+  // tile's first key stay below 64 row strides.
+  const uint32_t uw = __builtin_amdgcn_readfirstlane(wave);
+  const int crow = lane / 8;  // row within the 8-row group; (row & 7) == crow
+  const int kchunk = (lane % 8) ^ crow, vchunk = (lane % 8) ^ (2 * (crow & 3));
+  const bf16 *kseq = k + (int64_t)start * ks0 + (int64_t)hk * ks1;
+  const bf16 *vseq = v + (int64_t)start * vs0 + (int64_t)hk * vs1;
+  auto issue = [&](int kt, int stage) {
+    const bf16 *kb = kseq + (int64_t)kt * ks0, *vb = vseq + (int64_t)kt * vs0;
+    const uint32_t lk = lds_address(kv_lds[stage]) + uw * 2 * 1024, lv = lk + kBK * kRowBytes;
 #pragma unroll
-    for (int r = 0; r < kStage; ++r) {
-      const int64_t row = min(kt + skey + 32 * r, len - 1);
-      kv[r] = *reinterpret_cast<const u32x4 *>(kbase + row * ks0);
-      vv[r] = *reinterpret_cast<const u32x4 *>(vbase + row * vs0);
+    for (int i = 0; i < 2; ++i) {
+      const int row = min(8 * (2 * wave + i) + crow, len - 1 - kt);
+      lds_copy16(kb, (uint32_t)(row * ks0 + kchunk * 8) * 2, lk + i * 1024);
+      lds_copy16(vb, (uint32_t)(row * vs0 + vchunk * 8) * 2, lv + i * 1024);
     }
   };
   // Transposing-read addresses: lane 16g + 4j + t reads channels 4t..4t+3
   // (plus 16 per channel block) of key row 4g + j (slots 0-3) or
-  // 16 + 4g + j (slots 4-7), matching the keys of the P fragment.
-  const int trow = 4 * grp + (col / 4), tch = 4 * (col % 4);
-  u32x4 kv[kStage], vv[kStage];
-  load(0, kv, vv);
-  for (int kt = 0; kt < kend; kt += kBK) {
-    __syncthreads();  // the previous tile is no longer read
-#pragma unroll
-    for (int r = 0; r < kStage; ++r) {
-      *reinterpret_cast<u32x4 *>(&ks_lds[skey + 32 * r][sdc * 8]) = kv[r];
-      *reinterpret_cast<u32x4 *>(&vs_lds[skey + 32 * r][sdc * 8]) = vv[r];
-    }
+  // 16 + 4g + j (slots 4-7), matching the keys of the P fragment. Channel
+  // block d's bytes of that row are chunk 2d + t/2, offset 8 (t & 1).
+  const int trow = 4 * grp + (col / 4), tsub = (col % 4) / 2, toff = 8 * (col & 1);
+  int it = 0;
+  issue(0, 0);
+  for (int kt = 0; kt < kend; kt += kBK, ++it) {
+    // Tile it has landed in every wave, and every wave has left tile it - 1,
+    // whose stage the next copy overwrites.
+    lds_copy_wait();
     __syncthreads();
-    // The next tile streams in while this one is computed.
-    load(min(kt + kBK, kend - 1), kv, vv);
+    if (kt + kBK < kend) issue(kt + kBK, (it + 1) & 1);
     if (!wave_live || (causal && kt > wq0 + 16 * kQS - 1)) continue;
+    const char *ks = kv_lds[it & 1];
+    const char *vs = ks + kBK * kRowBytes;
     constexpr int kH = kBK / 16;  // 16-key blocks of the tile
     f32x4 st[kQS][kH];
-    u32x4 qf0[kQS], qf1[kQS];
-#pragma unroll
-    for (int qs = 0; qs < kQS; ++qs) {
-      qf0[qs] = qs_lds[wave][qs][0][lane];
-      qf1[qs] = qs_lds[wave][qs][1][lane];
-    }
 #pragma unroll
     for (int h = 0; h < kH; ++h) {
-      const u32x4 a0 = *reinterpret_cast<const u32x4 *>(&ks_lds[16 * h + col][grp * 8]);
-      const u32x4 a1 = *reinterpret_cast<const u32x4 *>(&ks_lds[16 * h + col][32 + grp * 8]);
+      const char *krow = ks + (16 * h + col) * kRowBytes;
+      const u32x4 a0 = *reinterpret_cast<const u32x4 *>(krow + ((grp ^ (col & 7)) << 4));
+      const u32x4 a1 = *reinterpret_cast<const u32x4 *>(krow + (((4 + grp) ^ (col & 7)) << 4));
 #pragma unroll
       for (int qs = 0; qs < kQS; ++qs) {
         st[qs][h] = mfma16x16x32(a0, qf0[qs], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -227,8 +231,10 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
       }
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const uint2 lo = read_tr(&vs_lds[32 * c + trow][d * 16 + tch]);
-        const uint2 hi = read_tr(&vs_lds[32 * c + 16 + trow][d * 16 + tch]);
+        const int r0 = 32 * c + trow, r1 = r0 + 16;  // (r & 3) == (col / 4) for both
+        const int pos = ((2 * d + tsub) ^ (2 * (col / 4))) << 4;
+        const uint2 lo = read_tr(reinterpret_cast<const bf16 *>(vs + r0 * kRowBytes + pos + toff));
+        const uint2 hi = read_tr(reinterpret_cast<const bf16 *>(vs + r1 * kRowBytes + pos + toff));
         const u32x4 vb = {lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
         for (int qs = 0; qs < kQS; ++qs) {
@@ -247,7 +253,9 @@ prefill_kernel(const bf16 *__restrict__ q, int64_t qs0, int64_t qs1, const bf16 
   // four lane groups of one write (rows 4 apart) then hit different banks.
   // l >= 1 for every query that has a key (its maximum key has p >= 1), and
   // the reciprocal (within one ulp) times O replaces a division per output.
-  uint16_t *tile = reinterpret_cast<uint16_t *>(qs_lds[wave]);
+  // The stage the last tile did not use: every wave left it at the barrier
+  // of the last tile, and no copy targets it. 4 KB per wave.
+  uint16_t *tile = reinterpret_cast<uint16_t *>(kv_lds[it & 1] + wave * (16 * kQS * kD * 2));
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
   for (int qs = 0; qs < kQS; ++qs) {
