@@ -123,6 +123,31 @@ def test_invalid_arguments_rejected_on_host(call, expected):
      1),
     ("routes packed workspace short", lambda h: h.lm_moe_routes_packed(_P, _P, _P, _P, 64, 1536, 512, 40, 8, 0, _P,
                                                                          _P, 4096, None), 4),
+    # QKV projection with the RoPE/KV epilogue: K not a multiple of 64, misaligned output, one cache pointer
+    ("rope_kv K 96", lambda h: h.lm_linear_rope_kv(_P, 96, _P, 4, 24, 8, 96, _P, 2560, _P, None, None, _P, 64,
+                                                     _P, _P, 64, 1, None), 2),
+    ("rope_kv out misaligned", lambda h: h.lm_linear_rope_kv(_P, 128, _P, 4, 24, 8, 128, _P + 4, 2560, _P, None,
+                                                               None, _P, 64, _P, _P, 64, 1, None), 1),
+    ("rope_kv one cache", lambda h: h.lm_linear_rope_kv(_P, 128, _P, 4, 24, 8, 128, _P, 2560, _P, None, None, _P,
+                                                          64, _P, None, 64, 1, None), 1),
+    ("rope_kv ldo short", lambda h: h.lm_linear_rope_kv(_P, 128, _P, 4, 24, 8, 128, _P, 2048, _P, None, None, _P,
+                                                          64, _P, _P, 64, 1, None), 1),
+    ("ok: rope_kv zero rows", lambda h: h.lm_linear_rope_kv(None, 128, None, 0, 24, 8, 128, None, 2560, None, None,
+                                                              None, None, 64, None, None, 64, 1, None), 0),
+    # chained decode: residual and out both given, topk 9, outside the scan path, short workspace
+    ("combine residual and out", lambda h: h.lm_moe_routes_combine(_P, _P, _P, _P, _P, 64, 1536, 512, 40, 8, _P,
+                                                                     C.c_float(0.2), _P, _P, _P, 1 << 30, None), 1),
+    ("combine topk 9", lambda h: h.lm_moe_routes_combine(_P, _P, _P, _P, _P, 64, 1536, 512, 40, 9, None,
+                                                           C.c_float(0.0), None, _P, _P, 1 << 30, None), 1),
+    ("combine 300 tokens", lambda h: h.lm_moe_routes_combine_packed(_P, _P, _P, _P, _P, 300, 1536, 512, 40, 8,
+                                                                      None, C.c_float(0.0), None, _P, _P, 1 << 30,
+                                                                      None), 2),
+    ("combine workspace short", lambda h: h.lm_moe_routes_combine(_P, _P, _P, _P, _P, 64, 1536, 512, 40, 8, None,
+                                                                    C.c_float(0.0), None, _P, _P, 64, None), 4),
+    ("splitk_rmsnorm K 1536+64", lambda h: h.lm_linear_splitk_rmsnorm(_P, _P, _P, C.c_float(1e-6), _P, 64, 2560,
+                                                                        1600, 3, _P, None), 2),
+    ("splitk_rmsnorm null sumsq", lambda h: h.lm_linear_splitk_rmsnorm(_P, None, _P, C.c_float(1e-6), _P, 64,
+                                                                         2560, 1536, 3, _P, None), 1),
     ("ok: zero tokens", lambda h: h.lm_fused_experts(_P, _P, _P, _P, _P, None, 0, 1024, 512, 8, 2, 0, _P, _P, 0,
                                                        None), 0),
 ])
