@@ -113,6 +113,53 @@ def test_benchmark_shapes_prefill_and_decode_match_oracle(name):
 
 
 @torch.inference_mode()
+def test_decode_above_128_rows_matches_oracle():
+    """A decode batch of 136 rows on the cfg 3 layer shape (two layers): the
+    projections run on lm_linear (QKV with the RoPE/KV epilogue), attention
+    on lm_flash_decode, the experts on the grouped path and the head on
+    lm_linear; packed prefill first, then decode steps against the oracle's
+    production rounding (logits within rel-L2 2e-2, greedy argmax agreement),
+    and a graph-mode greedy generate that emits the oracle's first token."""
+    from litemoe_amd import synth
+    from litemoe_amd.config import preset
+    cfg = preset("granite-3b", num_hidden_layers=2)
+    w_gpu = synth.granite_weights(cfg, seed=5, device=DEV, method="torch")
+    w_cpu = {k: ([{n: t.cpu() for n, t in layer.items()} for layer in v] if k == "layers" else v.cpu())
+             for k, v in w_gpu.items()}
+    ep = ExpertParallel(1, 0, 4096, cfg.hidden_size, cfg.num_experts_per_tok, torch.bfloat16, DEV,
+                        HipFusedExperts())
+    cap, batch = 32, 136
+    model, ref = Granite(cfg, w_gpu, ep, cap), oracle.Granite(cfg, w_cpu, cap, fused=True)
+    assert model.decode_splits(batch) is None  # above the split-K kernels' 128 rows
+    prompts = synth.prompts(batch, synth.ragged_lengths(batch, 3, 12, 7), cfg.vocab_size, 8)
+    cache = KVCache(cfg, batch, cap, DEV, torch.bfloat16)
+    rcache = oracle.Cache(cfg, batch, cap, torch.bfloat16)
+    logits = packed_prefill_logits(model, prompts, cache)[:, 0].cpu()
+    expected = torch.cat([ref.prefill(p, rcache, j, last_only=True) for j, p in enumerate(prompts)])
+    assert rel_l2(logits, expected) < 2e-2
+    tokens = expected.argmax(-1)
+    lengths = torch.tensor([len(p) for p in prompts])
+    agree, steps = 0, 0
+    for step in range(3):
+        valid = torch.ones(batch, dtype=torch.bool)
+        valid[::17] = step < 1  # some rows stop after the first step
+        positions = torch.where(valid, lengths, 0)
+        got = model.forward(tokens[:, None].to(DEV), positions[:, None].to(DEV), valid[:, None].to(DEV),
+                            cache)[:, 0].cpu()
+        exp = ref.decode(tokens, positions, valid, rcache)
+        assert rel_l2(got[valid], exp[valid]) < 2e-2, step
+        agree += int((got.argmax(-1) == exp.argmax(-1))[valid].sum())
+        steps += int(valid.sum())
+        tokens = torch.where(valid, exp.argmax(-1), tokens)
+        lengths += valid
+    assert agree >= steps - 2
+    requests = [Request(str(j), p, 3) for j, p in enumerate(prompts)]
+    out, _ = OptimizedEngine(model, requests, ignore_eos=True, capacity=cap, mode="graph").generate()
+    first = expected.argmax(-1)
+    assert sum(out[str(j)][0] == int(first[j]) for j in range(batch)) >= batch - 2
+
+
+@torch.inference_mode()
 def test_engine_modes_identical_and_close_to_oracle_greedy():
     """Reference test_cuda_execution.py:102-133: graph and graph-async equal
     eager, repeated generate() calls agree, EOS/poll inside the graph."""
