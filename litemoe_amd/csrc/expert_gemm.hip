@@ -19,15 +19,15 @@
 // kWM x kWN, each (kTM/kWM) x (kTN/kWN) as 16 x 16 tiles of
 // v_mfma_f32_16x16x32_bf16.
 //
-// K runs in steps of 64: the next step's A rows (gathered through the route
-// list) and B rows are loaded into registers while the MFMAs run on the
-// current step's LDS tile, then stored to LDS (the other buffer with two
-// stages; the same one after a barrier with one). Direct global-to-LDS loads
-// would save the registers, but the compiler then waits for every load in
-// flight before each LDS read. An LDS row is 64 bf16 = 8 chunks of 16 bytes;
-// chunk c of tile row r sits at position c ^ (r & 7), so the 16 rows read by
-// one MFMA fragment load spread over the banks, and each wave's stores fill
-// 1 KB contiguously.
+// K runs in steps of 64. With two LDS stages (the large tile) the next
+// step's A rows (gathered through the route list: each lane's copy has its
+// own address) and B rows are copied from global memory straight into the
+// other stage (global_load_lds_dwordx4, lds_copy16) while the MFMAs run on
+// the current one; with one stage (the small tile) they are loaded into
+// registers meanwhile and stored to LDS after a barrier. An LDS row is 64
+// bf16 = 8 chunks of 16 bytes; chunk c of tile row r sits at position
+// c ^ (r & 7), so the 16 rows read by one MFMA fragment load spread over the
+// banks, and each wave instruction fills 1 KB contiguously.
 //
 // Reference: the expert math of litemoe/ops.py:43-47 (reference_experts) and
 // vLLM fused_experts at litemoe/ep.py:40-41.
@@ -47,9 +47,11 @@ constexpr int kRowBytes = kBK * 2;  // 128
 // - Large: 256 route rows x 256 B rows on 8 waves of 64 x 128 (4 x 2), two
 //   LDS stages (128 KB, one workgroup per CU): a wave's fragments feed 32
 //   MFMAs per 32-wide k step, half the LDS reads per MFMA of a 64 x 64 wave
-//   tile. At cfg 4's 46,990 tokens (uniform routes, one box): gate/up 1230
-//   against 1561 us, down 912 against 1063 us for the small tile; 16 waves of
-//   64 x 64 1339 / 936 us, 128 x 256 on 8 waves 1412 / 1071 us.
+//   tile. At cfg 4's 46,990 tokens (uniform routes, one box, register
+//   staging): gate/up 1230 against 1561 us, down 912 against 1063 us for the
+//   small tile; 16 waves of 64 x 64 1339 / 936 us, 128 x 256 on 8 waves
+//   1412 / 1071 us. With the direct copies the MoE takes 2.13 against 2.34
+//   ms; 16 waves of 64 x 64 (LM_EXPERT_LARGE_WN=4) are within 1% of 8.
 // - Small: 128 x 128 on 4 waves of 64 x 64, one LDS stage (33 KB, several
 //   workgroups per CU), for fewer than 1024 routes per expert, where a
 //   256-route block would be mostly padding.
