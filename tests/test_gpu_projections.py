@@ -101,7 +101,9 @@ def _fp32_product(a, w, chunk=8192):
     (46990, 1536, 1536),   # cfg 4 o_proj
     (65536, 2560, 1536),   # cfg 3 prefill QKV (64 prompts of 1024)
     (48, 49155, 1536),     # prefill LM head at the last positions: odd vocabulary, 2-byte stores
-    (1, 512, 1024), (17, 200, 256), (130, 2560, 1536), (257, 1536, 1536)])
+    (1, 512, 1024), (17, 200, 256), (130, 2560, 1536), (257, 1536, 1536),
+    # one k step (K = 64) on both tile sizes, an odd column count on the 256-row tiles, two k steps
+    (2049, 100, 64), (5, 8, 64), (3000, 4100, 128), (2048, 2560, 192)])
 @torch.inference_mode()
 def test_linear_dense_matches_fp32_product(rows, n, k):
     """lm_linear against an fp32 product of the same bf16 operands: the bf16
