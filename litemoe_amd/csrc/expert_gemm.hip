@@ -280,16 +280,27 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   }
 
   // Transposed C fragment: lane holds output row lane%16 of each 16-row block
-  // and its output columns 4*(lane/16) .. +3 of each 16-column block, written
-  // as one 8-byte word. Intermediate roundings skip the NaN canonicalization
-  // (a NaN stays NaN through silu and the product, and the stored value is
-  // canonicalized).
+  // and its output columns 4*(lane/16) .. +3 of each 16-column block, one
+  // 8-byte word. Intermediate roundings skip the NaN canonicalization (a NaN
+  // stays NaN through silu and the product, and the stored value is
+  // canonicalized). The bf16 tile is staged in the (now idle) LDS stages and
+  // written out row by row in 16-byte words, so that a store instruction
+  // covers whole output rows (512 or 256 bytes each) instead of 32-byte
+  // pieces of 16 rows. Staged row r's 16-byte chunk c sits at c ^ (r & kSw):
+  // the 16 rows of one fragment store fall on different bank groups.
+  constexpr int kOutCols = kGateUp ? kTN / 2 : kTN, kOB = kOutCols * 2;  // output row bytes
+  constexpr int kChunks = kOB / 16, kSw = (kChunks < 16 ? kChunks : 16) - 1;
+  constexpr int kHalfRows = kStageBytes / kOB;  // rows held by the first stage
+  static_assert(kTM * kOB <= (kStages == 2 ? 2 : 1) * kStageBytes, "output tile fits the LDS stages");
+  auto staged = [&](int row) -> char * {
+    if constexpr (kTM <= kHalfRows) return smem + row * kOB;
+    else return row < kHalfRows ? smem + row * kOB : smem1 + (row - kHalfRows) * kOB;
+  };
+  __syncthreads();  // every wave has finished reading the stages
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) {
     const int row = wr * kWaveRows + rb * 16 + fr;
-    if (row >= n) continue;
-    const int64_t orow = kGateUp && kSortedAct ? r0 + row : route_of[row];
-    bf16 *o = out + orow * out_cols + c0 + 4 * fk;
+    char *srow = staged(row);
     if constexpr (kGateUp) {
 #pragma unroll
       for (int cb = 0; cb < kCB / 2; ++cb) {
@@ -297,14 +308,29 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           h[i] = round_bf16_nc(silu(round_bf16_nc(acc[rb][cb][i]))) * round_bf16_nc(acc[rb][cb + kCB / 2][i]);
-        *reinterpret_cast<uint2 *>(o + wc * kGateCols + cb * 16) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
+        const int byte = 2 * (wc * kGateCols + cb * 16 + 4 * fk);
+        *reinterpret_cast<uint2 *>(srow + (((byte >> 4) ^ (row & kSw)) << 4) + (byte & 8)) =
+            make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
       }
     } else {
 #pragma unroll
-      for (int cb = 0; cb < kCB; ++cb)
-        *reinterpret_cast<uint2 *>(o + wc * kWaveCols + cb * 16) =
+      for (int cb = 0; cb < kCB; ++cb) {
+        const int byte = 2 * (wc * kWaveCols + cb * 16 + 4 * fk);
+        *reinterpret_cast<uint2 *>(srow + (((byte >> 4) ^ (row & kSw)) << 4) + (byte & 8)) =
             make_uint2(pack_bf16(acc[rb][cb][0], acc[rb][cb][1]), pack_bf16(acc[rb][cb][2], acc[rb][cb][3]));
+      }
     }
+  }
+  __syncthreads();
+  static_assert((kTM * kChunks) % kThreadsT == 0, "whole store rounds");
+#pragma unroll
+  for (int i = 0; i < kTM * kChunks / kThreadsT; ++i) {
+    const int idx = i * kThreadsT + threadIdx.x;
+    const int row = idx / kChunks, c = idx % kChunks;
+    if (row >= n) continue;
+    const int64_t orow = kGateUp && kSortedAct ? r0 + row : route_of[row];
+    *reinterpret_cast<u32x4 *>(out + orow * out_cols + c0 + c * 8) =
+        *reinterpret_cast<const u32x4 *>(staged(row) + ((c ^ (row & kSw)) << 4));
   }
 }
 
