@@ -34,6 +34,8 @@
 //
 // Reference: the packed QKV and output projections of litemoe/model.py:47-49
 // and :60 (F.linear over the packed prefill rows), and the LM head :127.
+#include <type_traits>
+
 #include "internal.h"
 
 namespace lm {
@@ -67,9 +69,11 @@ __device__ __forceinline__ void rotate3(float x1, float x2, float c, float s, fl
   o2 = round_bf16(round_bf16(x2 * c) + round_bf16(x1 * s));
 }
 
-// kVec: ldo and out allow 8-byte stores and N % 4 == 0 (else 2-byte stores).
-// kRope: the RopeKV epilogue (64-column wave blocks, kVec).
-template <int kTM, int kTN, int kWM, int kWN, bool kVec, bool kRope = false>
+// kStore: 2 = whole rows in 16-byte words through LDS (N % 8 == 0, ldo % 8 == 0,
+// out 16-byte aligned), 1 = 8-byte fragment words (N % 4 == 0, ldo % 4 == 0,
+// out 8-byte aligned), 0 = 2-byte stores.
+// kRope: the RopeKV epilogue (64-column wave blocks, kStore >= 1).
+template <int kTM, int kTN, int kWM, int kWN, int kStore, bool kRope = false>
 __global__ void __launch_bounds__(64 * kWM * kWN)
 gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w, int64_t ldw,
             bf16 *__restrict__ out, int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n,
@@ -82,6 +86,8 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
   constexpr int kABytes = kTM * kRowBytes, kStage = (kTM + kTN) * kRowBytes;
   __shared__ __align__(16) char s0[kStage];  // two LDS stages
   __shared__ __align__(16) char s1[kStage];
+  __shared__ int64_t st_pos[kRope ? kTM : 1];  // kRope, kStore == 2: cache position per row
+  __shared__ int st_slot[kRope ? kTM : 1];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int lin = blockIdx.x;
   int tile_m = lin / tiles_n, tile_n = lin % tiles_n;
@@ -172,12 +178,106 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
 
   // Transposed C fragment: lane holds output row m0 + wr*kWaveRows + rb*16 +
   // lane%16 and its columns 4*(lane/16) .. +3 of each 16-column block.
+  // kRope: channel 16*cb + 4*fk + i and its neox partner (+32) sit in the
+  // same lane, blocks cb and cb + 2.
+  static_assert(!kRope || (kWaveCols == 64 && kStore >= 1), "one head per wave column block");
+  [[maybe_unused]] const int head = (n0 + wc * kWaveCols) / 64;  // kRope: uniform per wave
+  [[maybe_unused]] const bool rot = head < rk.q_heads + rk.kv_heads;
+  // Row block rb2's fragments for output row `row`: bf16-rounded and, for
+  // kRope, q and k rotated (values of rows past M are never stored).
+  auto values = [&](int rb2, int row, float (&v)[kCB][4]) {
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[cb][i] = kRope ? round_bf16(acc[rb2][cb][i]) : acc[rb2][cb][i];
+    if constexpr (kRope) {
+      if (!rot || row >= M) return;
+      const int64_t p = rk.pos[row];
+      if (p < 0 || p >= rk.table_len) return;
+      const bf16 *cs = rk.cos_sin + p * 64;
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const uint2 cw = *reinterpret_cast<const uint2 *>(cs + cb * 16 + 4 * fk);
+        const uint2 sw = *reinterpret_cast<const uint2 *>(cs + 32 + cb * 16 + 4 * fk);
+        const float c[4] = {lo_f32(cw.x), hi_f32(cw.x), lo_f32(cw.y), hi_f32(cw.y)};
+        const float sn[4] = {lo_f32(sw.x), hi_f32(sw.x), lo_f32(sw.y), hi_f32(sw.y)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rotate3(v[cb][i], v[cb + 2][i], c[i], sn[i], v[cb][i], v[cb + 2][i]);
+      }
+    }
+  };
+
+  if constexpr (kStore == 2) {
+    // The bf16 tile is staged in the (now idle) LDS stages and written out
+    // row by row in 16-byte words, so that a store instruction covers whole
+    // 512- or 256-byte row segments instead of 32-byte pieces of 16 rows.
+    // Staged row r's 16-byte chunk c sits at c ^ (r & kSw): the 16 rows of
+    // one fragment store fall on different bank groups.
+    constexpr int kOB = kTN * 2, kChunks = kOB / 16, kSw = (kChunks < 16 ? kChunks : 16) - 1;
+    constexpr int kHalfRows = kStage / kOB;  // rows held by the first stage
+    static_assert(kTM * kOB <= 2 * kStage, "output tile fits the LDS stages");
+    auto staged = [&](int r) -> char * {
+      if constexpr (kTM <= kHalfRows) return s0 + r * kOB;
+      else return r < kHalfRows ? s0 + r * kOB : s1 + (r - kHalfRows) * kOB;
+    };
+    __syncthreads();  // every wave has finished reading the stages
+    if constexpr (kRope) {
+      // Each row's cache position, or -1 where lm_kv_write's mask skips it.
+      for (int t = threadIdx.x; t < kTM; t += 64 * kWaves) {
+        const int row = m0 + t;
+        int64_t sp = -1;
+        int ss = 0;
+        if (row < M && rk.kc) {
+          const int64_t p = rk.pos[row];
+          const int64_t slot = rk.slots ? rk.slots[row] : row;
+          if ((!rk.active || rk.active[row]) && p >= 0 && p < rk.capacity && slot >= 0 &&
+              slot < rk.cache_batch) {
+            sp = p;
+            ss = (int)slot;
+          }
+        }
+        st_pos[t] = sp;
+        st_slot[t] = ss;
+      }
+    }
+#pragma unroll
+    for (int rb2 = 0; rb2 < kRB; ++rb2) {
+      const int rl = wr * kWaveRows + rb2 * 16 + fr;
+      float v[kCB][4];
+      values(rb2, m0 + rl, v);
+      char *srow = staged(rl);
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        const int byte = 2 * (wc * kWaveCols + cb * 16 + 4 * fk);
+        *reinterpret_cast<uint2 *>(srow + (((byte >> 4) ^ (rl & kSw)) << 4) + (byte & 8)) =
+            make_uint2(pack_bf16(v[cb][0], v[cb][1]), pack_bf16(v[cb][2], v[cb][3]));
+      }
+    }
+    __syncthreads();
+    static_assert((kTM * kChunks) % (64 * kWaves) == 0, "whole store rounds");
+#pragma unroll
+    for (int i = 0; i < kTM * kChunks / (64 * kWaves); ++i) {
+      const int idx = i * 64 * kWaves + threadIdx.x;
+      const int rl = idx / kChunks, c = idx % kChunks;
+      const int row = m0 + rl, col = n0 + c * 8;
+      if (row >= M || col >= N) continue;
+      const u32x4 word = *reinterpret_cast<const u32x4 *>(staged(rl) + ((c ^ (rl & kSw)) << 4));
+      *reinterpret_cast<u32x4 *>(out + (int64_t)row * ldo + col) = word;
+      if constexpr (kRope) {
+        const int h = col / 64 - rk.q_heads;  // k heads, then v heads
+        const int64_t sp = st_pos[rl];
+        if (h >= 0 && h < 2 * rk.kv_heads && sp >= 0) {
+          const bool is_k = h < rk.kv_heads;
+          const int kvh = is_k ? h : h - rk.kv_heads;
+          bf16 *dst = (is_k ? rk.kc : rk.vc) + (((int64_t)st_slot[rl] * rk.kv_heads + kvh) * rk.capacity + sp) * 64;
+          *reinterpret_cast<u32x4 *>(dst + col % 64) = word;
+        }
+      }
+    }
+    return;
+  }
   if constexpr (kRope) {
-    static_assert(kWaveCols == 64 && kVec, "one head per wave column block");
-    // Channel 16*cb + 4*fk + i and its neox partner (+32) sit in the same
-    // lane, blocks cb and cb + 2.
-    const int head = (n0 + wc * kWaveCols) / 64;  // uniform per wave
-    const bool rot = head < rk.q_heads + rk.kv_heads, is_k = rot && head >= rk.q_heads;
+    const bool is_k = rot && head >= rk.q_heads;
     const int kvh = rot ? head - rk.q_heads : head - rk.q_heads - rk.kv_heads;
     bf16 *cache = is_k ? rk.kc : rk.vc;
 #pragma unroll
@@ -188,23 +288,8 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
       const int64_t slot = rk.slots ? rk.slots[row] : row;
       const bool store = (is_k || !rot) && cache && (!rk.active || rk.active[row]) && p >= 0 &&
                          p < rk.capacity && slot >= 0 && slot < rk.cache_batch;
-      float v[4][4];
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[cb][i] = round_bf16(acc[rb2][cb][i]);
-      if (rot && p >= 0 && p < rk.table_len) {
-        const bf16 *cs = rk.cos_sin + p * 64;
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          const uint2 cw = *reinterpret_cast<const uint2 *>(cs + cb * 16 + 4 * fk);
-          const uint2 sw = *reinterpret_cast<const uint2 *>(cs + 32 + cb * 16 + 4 * fk);
-          const float c[4] = {lo_f32(cw.x), hi_f32(cw.x), lo_f32(cw.y), hi_f32(cw.y)};
-          const float sn[4] = {lo_f32(sw.x), hi_f32(sw.x), lo_f32(sw.y), hi_f32(sw.y)};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) rotate3(v[cb][i], v[cb + 2][i], c[i], sn[i], v[cb][i], v[cb + 2][i]);
-        }
-      }
+      float v[kCB][4];
+      values(rb2, row, v);
       bf16 *o = out + (int64_t)row * ldo + n0 + wc * kWaveCols + 4 * fk;
       bf16 *dst = store ? cache + ((slot * rk.kv_heads + kvh) * rk.capacity + p) * 64 + 4 * fk : nullptr;
 #pragma unroll
@@ -225,7 +310,7 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
     for (int cb = 0; cb < kCB; ++cb) {
       const int col = n0 + wc * kWaveCols + cb * 16 + 4 * fk;
       const f32x4 v = acc[rb2][cb];
-      if constexpr (kVec) {
+      if constexpr (kStore == 1) {
         if (col < N)
           *reinterpret_cast<uint2 *>(o + col) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
       } else {
@@ -246,17 +331,27 @@ int launch_gemm_cfg(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16
   const bool remap = tiles_m >= kXcds;
   const int64_t blocks = (remap ? align_up(tiles_m, kXcds) : tiles_m) * tiles_n;
   const bool vec = N % 4 == 0 && ldo % 4 == 0 && ((uintptr_t)out & 7) == 0;
+  const bool vec16 = N % 8 == 0 && ldo % 8 == 0 && ((uintptr_t)out & 15) == 0;
   const dim3 grid((unsigned)blocks);
+  auto go = [&](auto store_c, auto rope_c) {
+    gemm_kernel<TM, TN, WM, WN, decltype(store_c)::value, decltype(rope_c)::value>
+        <<<grid, 64 * WM * WN, 0, stream>>>(a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K,
+                                            (int)tiles_m, (int)tiles_n, (int)remap,
+                                            rope ? *rope : RopeKV{});
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
   if (rope) {
     if (!vec) return LM_EINVAL;
-    gemm_kernel<TM, TN, WM, WN, true, true><<<grid, 64 * WM * WN, 0, stream>>>(
-        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap, *rope);
+    if (vec16) go(S2{}, std::true_type{});
+    else go(S1{}, std::true_type{});
+  } else if (vec16) {
+    go(S2{}, std::false_type{});
   } else if (vec) {
-    gemm_kernel<TM, TN, WM, WN, true><<<grid, 64 * WM * WN, 0, stream>>>(
-        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap, RopeKV{});
+    go(S1{}, std::false_type{});
   } else {
-    gemm_kernel<TM, TN, WM, WN, false><<<grid, 64 * WM * WN, 0, stream>>>(
-        a, lda, w, ldw, out, ldo, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)remap, RopeKV{});
+    go(S0{}, std::false_type{});
   }
   LM_CHECK_LAUNCH();
   return LM_OK;
