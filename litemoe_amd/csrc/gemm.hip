@@ -159,6 +159,27 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
   // Before a stage is read: this wave's copies have landed (vmcnt) and the
   // barrier has seen every wave's, and every wave has left the step that
   // last read the stage the next copy goes into.
+  // kRope with staged stores: the positions of this lane's fragment rows and
+  // the cache position of tile row threadIdx.x % kTM are requested before the
+  // K loop (unconditional loads, rows clamped into [0, M)), so the epilogue
+  // does not wait on them.
+  constexpr bool kPre = kRope && kStore == 2;
+  [[maybe_unused]] int64_t frag_pos[kPre ? kRB : 1];
+  [[maybe_unused]] int64_t pre_pos = -1;
+  [[maybe_unused]] int pre_slot = 0;
+  if constexpr (kPre) {
+#pragma unroll
+    for (int rb2 = 0; rb2 < kRB; ++rb2) frag_pos[rb2] = rk.pos[min(m0 + wr * kWaveRows + rb2 * 16 + fr, M - 1)];
+    const int row = m0 + (int)(threadIdx.x % kTM), rc = min(row, M - 1);
+    const int64_t p = rk.pos[rc];
+    const int64_t slot = rk.slots ? rk.slots[rc] : rc;
+    const bool act = rk.active ? rk.active[rc] != 0 : true;
+    if (row < M && rk.kc && act && p >= 0 && p < rk.capacity && slot >= 0 && slot < rk.cache_batch) {
+      pre_pos = p;
+      pre_slot = (int)slot;
+    }
+  }
+
   const int nk = K / kBK;
   issue(0, s0);
   for (int kt = 0; kt < nk; kt += 2) {
@@ -221,30 +242,54 @@ gemm_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w,
       else return r < kHalfRows ? s0 + r * kOB : s1 + (r - kHalfRows) * kOB;
     };
     __syncthreads();  // every wave has finished reading the stages
+    [[maybe_unused]] uint2 csw[kPre ? kRB : 1][4];
     if constexpr (kRope) {
       // Each row's cache position, or -1 where lm_kv_write's mask skips it.
-      for (int t = threadIdx.x; t < kTM; t += 64 * kWaves) {
-        const int row = m0 + t;
-        int64_t sp = -1;
-        int ss = 0;
-        if (row < M && rk.kc) {
-          const int64_t p = rk.pos[row];
-          const int64_t slot = rk.slots ? rk.slots[row] : row;
-          if ((!rk.active || rk.active[row]) && p >= 0 && p < rk.capacity && slot >= 0 &&
-              slot < rk.cache_batch) {
-            sp = p;
-            ss = (int)slot;
-          }
-        }
-        st_pos[t] = sp;
-        st_slot[t] = ss;
+      if (threadIdx.x < kTM) {
+        st_pos[threadIdx.x] = pre_pos;
+        st_slot[threadIdx.x] = pre_slot;
+      }
+      // cos | sin of every fragment row's channels, requested together (the
+      // position clamped into the table; rows outside it are not rotated).
+#pragma unroll
+      for (int rb2 = 0; rb2 < kRB; ++rb2) {
+        const bf16 *cs = rk.cos_sin + min(max(frag_pos[rb2], (int64_t)0), rk.table_len - 1) * 64 + 4 * fk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) csw[rb2][i] = *reinterpret_cast<const uint2 *>(cs + 16 * i);
       }
     }
 #pragma unroll
     for (int rb2 = 0; rb2 < kRB; ++rb2) {
       const int rl = wr * kWaveRows + rb2 * 16 + fr;
       float v[kCB][4];
-      values(rb2, m0 + rl, v);
+      if constexpr (kRope) {
+        // The rotation's roundings skip the NaN canonicalization: every value
+        // is canonicalized by the packing below.
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[cb][i] = round_bf16_nc(acc[rb2][cb][i]);
+        // Rotated unconditionally and selected, so that no load or wait
+        // moves under a branch.
+        const int64_t p = frag_pos[rb2];
+        const bool ok = rot && p >= 0 && p < rk.table_len;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const uint2 cw = csw[rb2][cb], sw = csw[rb2][cb + 2];
+          const float c[4] = {lo_f32(cw.x), hi_f32(cw.x), lo_f32(cw.y), hi_f32(cw.y)};
+          const float sn[4] = {lo_f32(sw.x), hi_f32(sw.x), lo_f32(sw.y), hi_f32(sw.y)};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float x1 = v[cb][i], x2 = v[cb + 2][i];
+            const float o1 = round_bf16_nc(round_bf16_nc(x1 * c[i]) - round_bf16_nc(x2 * sn[i]));
+            const float o2 = round_bf16_nc(round_bf16_nc(x2 * c[i]) + round_bf16_nc(x1 * sn[i]));
+            v[cb][i] = ok ? o1 : x1;
+            v[cb + 2][i] = ok ? o2 : x2;
+          }
+        }
+      } else {
+        values(rb2, m0 + rl, v);
+      }
       char *srow = staged(rl);
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb) {
@@ -344,7 +389,7 @@ int launch_gemm_cfg(const bf16 *a, int64_t lda, const bf16 *w, int64_t ldw, bf16
   using S2 = std::integral_constant<int, 2>;
   if (rope) {
     if (!vec) return LM_EINVAL;
-    if (vec16) go(S2{}, std::true_type{});
+    if (vec16 && rope->table_len > 0) go(S2{}, std::true_type{});
     else go(S1{}, std::true_type{});
   } else if (vec16) {
     go(S2{}, std::false_type{});
