@@ -872,34 +872,89 @@ align_chunk_kernel(const int32_t *__restrict__ ids, int routes, int first, int l
 }
 
 // One workgroup: offsets[k] = routes with a smaller key; bases[c][k] =
-// offsets[k] + routes of key k in chunks before c.
-__global__ void __launch_bounds__(kAlignThreads)
+// offsets[k] + routes of key k in chunks before c. Lane l takes key 64*g + l
+// (key groups g of 64), wave w the chunks [w*per, (w+1)*per): a load reads
+// one chunk's counts of 64 adjacent keys, and a wave's up to kScanRegs counts
+// per key are held in LDS from the sum to the writes. (One thread per key
+// walking every chunk waits on one load round trip per eight chunks.) With
+// 24 counts per lane in flight at once, up to 384 chunks (393,216 routes) take
+// one load round trip.
+constexpr int kScanWaves = 16, kScanRegs = 24;
+__global__ void __launch_bounds__(kScanWaves * kWave)
 align_scan_kernel(const int32_t *__restrict__ counts, int chunks, int keys,
                   int32_t *__restrict__ bases, int32_t *__restrict__ offsets) {
-  __shared__ int scan[2][kAlignThreads];
-  const int k = threadIdx.x;
-  int total = 0;
-  if (k < keys) {
-#pragma unroll 8
-    for (int c = 0; c < chunks; ++c) total += counts[(int64_t)c * keys + k];
-  }
-  scan[0][k] = k < keys ? total : 0;
-  __syncthreads();
-  int src = 0;
-  for (int d = 1; d < kAlignThreads; d <<= 1) {
-    scan[1 - src][k] = scan[src][k] + (k >= d ? scan[src][k - d] : 0);
-    src = 1 - src;
-    __syncthreads();
-  }
-  if (k < keys) {
-    int running = scan[src][k] - total;  // exclusive
-    offsets[k] = running;
-#pragma unroll 8
-    for (int c = 0; c < chunks; ++c) {
-      const int v = counts[(int64_t)c * keys + k];
-      bases[(int64_t)c * keys + k] = running;
-      running += v;
+  __shared__ int part[kScanWaves][kWave];  // per wave and key: sum, then exclusive prefix over waves
+  __shared__ int key_base[kWave];
+  __shared__ int held[kScanWaves * kScanRegs][kWave];  // the counts, from the sum to the writes
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int per = (chunks + kScanWaves - 1) / kScanWaves;
+  const int c0 = wave * per, c1 = min(c0 + per, chunks);
+  int carry = 0;  // wave 0: routes of the key groups before g
+  for (int g = 0; g * kWave < keys; ++g) {
+    const int k = g * kWave + lane, kc = min(k, keys - 1);
+    const bool key_ok = k < keys;
+    int sum = 0;
+    if (per <= kScanRegs) {
+      // one pointer stepped a chunk at a time, held at the last chunk of the range
+      const int32_t *src = counts + (int64_t)min(c0, chunks - 1) * keys + kc;
+      int v[kScanRegs];
+#pragma unroll
+      for (int i = 0; i < kScanRegs; ++i) {
+        v[i] = *src;
+        src += c0 + i + 1 < c1 ? keys : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < kScanRegs; ++i) {
+        v[i] = c0 + i < c1 ? v[i] : 0;
+        sum += v[i];
+        held[wave * kScanRegs + i][lane] = v[i];
+      }
+    } else {
+      for (int c = c0; c < c1; c += 8) {
+        int w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = counts[(int64_t)min(c + i, c1 - 1) * keys + kc];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += c + i < c1 ? w[i] : 0;
+      }
     }
+    part[wave][lane] = key_ok ? sum : 0;
+    __syncthreads();
+    if (wave == 0) {
+      int total = 0;
+#pragma unroll
+      for (int w = 0; w < kScanWaves; ++w) {
+        const int x = part[w][lane];
+        part[w][lane] = total;
+        total += x;
+      }
+      int incl = total;
+#pragma unroll
+      for (int d = 1; d < kWave; d *= 2) {
+        const int up = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += up;
+      }
+      const int excl = carry + incl - total;
+      if (key_ok) offsets[k] = excl;
+      key_base[lane] = excl;
+      carry += __shfl(incl, kWave - 1, kWave);
+    }
+    __syncthreads();
+    if (key_ok) {
+      int running = key_base[lane] + part[wave][lane];
+      if (per <= kScanRegs) {
+        for (int c = c0; c < c1; ++c) {
+          bases[(int64_t)c * keys + k] = running;
+          running += held[wave * kScanRegs + c - c0][lane];
+        }
+      } else {
+        for (int c = c0; c < c1; ++c) {
+          bases[(int64_t)c * keys + k] = running;
+          running += counts[(int64_t)c * keys + k];
+        }
+      }
+    }
+    __syncthreads();  // part and key_base are reused by the next key group
   }
 }
 
@@ -1043,7 +1098,7 @@ int launch_align(const int32_t *ids, int64_t routes, int64_t first_expert, int64
     int32_t *counts = scratch, *bases = scratch + (int64_t)chunks * keys;
     align_chunk_kernel<false><<<chunks, kChunk, wave_bytes, stream>>>(
         ids, (int)routes, (int)first_expert, (int)local_experts, counts, nullptr, nullptr, nullptr);
-    align_scan_kernel<<<1, kAlignThreads, 0, stream>>>(counts, chunks, keys, bases, offsets);
+    align_scan_kernel<<<1, kScanWaves * kWave, 0, stream>>>(counts, chunks, keys, bases, offsets);
     align_chunk_kernel<true><<<chunks, kChunk, wave_bytes, stream>>>(
         ids, (int)routes, (int)first_expert, (int)local_experts, nullptr, bases, sorted, inverse);
   } else {
