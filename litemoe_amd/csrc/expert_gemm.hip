@@ -150,8 +150,19 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
   if (!block_of(offsets, experts, kTM, tile_y, e, r0, r1)) return;
   const int n = r1 - r0;
   const int c0 = tile_x * (kGateUp ? kTN / 2 : kTN);  // first output column
-  for (int t = threadIdx.x; t < kTM; t += kThreadsT) route_of[t] = sorted[r0 + min(t, n - 1)];
-  __syncthreads();
+  // The route list in LDS serves the A row offsets of gate_up and of down on
+  // route-order act, and y's rows in down's epilogue. gate_up on sorted act
+  // reads each row's route directly (no LDS round, no barrier); down on
+  // sorted act fills the list only after its first k step's copies are out
+  // (its rows are the block's own), so the two load round trips overlap.
+  constexpr bool kRouteList = !(kGateUp && kSortedAct), kListFirst = !kSortedAct;
+  auto fill_routes = [&]() {
+    for (int t = threadIdx.x; t < kTM; t += kThreadsT) route_of[t] = sorted[r0 + min(t, n - 1)];
+  };
+  if constexpr (kListFirst) {
+    fill_routes();
+    __syncthreads();
+  }
 
   // Load instruction i of wave w fills LDS rows 8*(w*L+i) .. +7 of an
   // operand (1 KB, lane l at byte 16*l): row 8*(w*L+i) + l/8, position l%8,
@@ -164,7 +175,7 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
     if constexpr (!kGateUp && kSortedAct) {
       oa[i] = (r0 + min(t, n - 1)) * K + chunk * 8;
     } else {
-      const int route = route_of[t];
+      const int route = kListFirst ? route_of[t] : sorted[r0 + min(t, n - 1)];
       oa[i] = (kGateUp ? route / topk : route) * K + chunk * 8;
     }
   }
@@ -250,6 +261,8 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
     // barrier has seen every wave's, and every wave has left the step that
     // last read the stage the next copy goes into.
     issue(0, smem);
+    // published by the first barrier below; read only in the epilogue
+    if constexpr (kRouteList && !kListFirst) fill_routes();
     for (int kt = 0; kt < nk; kt += 2) {
       lds_copy_wait();
       __syncthreads();
@@ -266,6 +279,7 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
     }
   } else {
     load(0);
+    if constexpr (kRouteList && !kListFirst) fill_routes();
     store();
     __syncthreads();
     for (int kt = 0; kt + 1 < nk; ++kt) {
