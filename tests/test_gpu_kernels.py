@@ -335,6 +335,29 @@ def test_prefill_expert_gemm_and_chunked_align_match_oracle(m, h, i, e, k, skew)
     assert float(per_row.max()) < 5e-2
 
 
+@pytest.mark.parametrize("m,e", [(50000, 40), (13000, 96)])
+@torch.inference_mode()
+def test_chunked_align_long_and_wide_scans_match_oracle(m, e):
+    """The chunked align's scan beyond 384 chunks of 1024 routes (400,000
+    routes: its looped form) and with more than 64 expert keys (97: two key
+    groups), under the 256-route expert GEMMs: the routes of 256 sampled
+    tokens against the oracle's per-route expert math (a wrong permutation
+    sends a route to another expert's weights or its row to another route)."""
+    h, i, k = 256, 128, 8
+    g = torch.Generator().manual_seed(m + e)
+    x = torch.randn(m, h, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(e, 2 * i, h, generator=g) * 0.05).to(torch.bfloat16)
+    w2 = (torch.randn(e, h, i, generator=g) * 0.05).to(torch.bfloat16)
+    ids = torch.rand(m, e, generator=g).argsort(dim=1)[:, :k].to(torch.int32)
+    y = experts.moe_routes(x.to(DEV), w1.to(DEV), w2.to(DEV), ids.to(DEV)).cpu()
+    sample = torch.randperm(m, generator=g)[:256]
+    exp = ops.expert_routes(x[sample], ids[sample], w1, w2)
+    got = y.view(m, k, h)[sample].reshape(-1, h)
+    assert rel_l2(got, exp) < 1e-2
+    per_row = (got.float() - exp.float()).norm(dim=1) / exp.float().norm(dim=1).clamp_min(1e-6)
+    assert float(per_row.max()) < 5e-2
+
+
 @torch.inference_mode()
 def test_prefill_expert_gemm_close_to_block_kernels():
     """The GEMM path (block_rows=0) against the per-tile block kernels
