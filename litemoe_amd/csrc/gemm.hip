@@ -23,9 +23,13 @@
 // position c ^ (r & 7), so the 16 rows of one fragment read spread over the
 // banks, and each copy instruction fills 1 KB contiguously. At the cfg 4 QKV
 // shape (46,990 x 1536 -> 2560, one box) the copies take the projection from
-// 472 to 365 us against register staging; at the o_proj shape 261 -> 220 us. The weights are the MFMA's first operand, so a lane ends with
-// four consecutive output columns of one row and stores them as one 8-byte
-// word.
+// 472 to 365 us against register staging; at the o_proj shape 261 -> 220 us.
+// The weights are the MFMA's first operand, so a lane ends with four
+// consecutive output columns of one row. When the output rows allow 16-byte
+// stores, the bf16 tile is staged in the idle LDS stages and each store
+// instruction writes whole row segments (the QKV shape 333 -> 320 us, the
+// cfg 4 prefill 104.0 -> 103.0-103.3 ms); otherwise each lane stores its four
+// columns as one 8-byte word (or 2-byte stores for odd widths).
 //
 // Workgroups are dealt to the 8 XCDs round-robin in launch order; they are
 // remapped so each XCD takes a contiguous range of row tiles with all their
