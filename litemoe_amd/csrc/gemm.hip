@@ -27,8 +27,8 @@
 // The weights are the MFMA's first operand, so a lane ends with four
 // consecutive output columns of one row. When the output rows allow 16-byte
 // stores, the bf16 tile is staged in the idle LDS stages and each store
-// instruction writes whole row segments (the QKV shape 333 -> 320 us, the
-// cfg 4 prefill 104.0 -> 103.0-103.3 ms); otherwise each lane stores its four
+// instruction writes whole row segments (the cfg 4 prefill 104.0 ->
+// 103.0-103.3 ms, A/B on one box); otherwise each lane stores its four
 // columns as one 8-byte word (or 2-byte stores for odd widths).
 //
 // Workgroups are dealt to the 8 XCDs round-robin in launch order; they are
