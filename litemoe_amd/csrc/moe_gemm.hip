@@ -139,6 +139,15 @@ __device__ __forceinline__ void xcd_tile(int &e, int &tile) {
 }
 
 __device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
+// Expert weight tiles of the decode scan kernels: each 16-byte word is read
+// by one workgroup once per step, so the load is marked non-temporal (the
+// weights need no room in L2 or the memory-side cache, which keep the
+// activations and the partial results instead): the decode step at cfg 3
+// 2.976 -> 2.903 ms, the MoE 45.8 -> 43.6-44.0 us per layer (A/B on one box,
+// two runs each).
+__device__ __forceinline__ u32x4 load16_stream(const bf16 *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
 
 struct RouteSet {
   const int32_t *sorted;  // blocks mode: route of sorted position p
@@ -269,8 +278,8 @@ gate_up_scan_kernel(const bf16 *__restrict__ x, const bf16 *__restrict__ w13,
   __builtin_amdgcn_sched_barrier(0);  // ids first: the scan waits for them only
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    bg[s] = load16(wg + s * wstep<kPacked>());
-    bu[s] = load16(wu + s * wstep<kPacked>());
+    bg[s] = load16_stream(wg + s * wstep<kPacked>());
+    bu[s] = load16_stream(wu + s * wstep<kPacked>());
   }
   __builtin_amdgcn_sched_barrier(0);
   const int n = scan_ids(scan, e, list, wave_count);
@@ -585,7 +594,7 @@ down_scan_kernel(const bf16 *__restrict__ act, const bf16 *__restrict__ w2,
   for (int t = 0; t < NT; ++t) {
     const bf16 *wt = w2 + wofs<kPacked>(r0 + 16 * t, kbase, inter);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) b[t][s] = load16(wt + s * wstep<kPacked>());
+    for (int s = 0; s < KS; ++s) b[t][s] = load16_stream(wt + s * wstep<kPacked>());
   }
   __builtin_amdgcn_sched_barrier(0);
   const int n = scan_ids(scan, e, list, wave_count);
