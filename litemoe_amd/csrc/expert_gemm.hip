@@ -343,8 +343,12 @@ expert_gemm_kernel(const bf16 *__restrict__ a_src, const bf16 *__restrict__ w,
     const int row = idx / kChunks, c = idx % kChunks;
     if (row >= n) continue;
     const int64_t orow = kGateUp && kSortedAct ? r0 + row : route_of[row];
-    *reinterpret_cast<u32x4 *>(out + orow * out_cols + c0 + c * 8) =
-        *reinterpret_cast<const u32x4 *>(staged(row) + ((c ^ (row & kSw)) << 4));
+    // Non-temporal: act and y are written once and read once by the next
+    // launch, far more bytes (0.4 and 1.2 GB at cfg 4) than the caches hold
+    // (the cfg 4 prefill 102.8 -> 100.1-100.5 ms, A/B on one box, three runs
+    // each).
+    __builtin_nontemporal_store(*reinterpret_cast<const u32x4 *>(staged(row) + ((c ^ (row & kSw)) << 4)),
+                                reinterpret_cast<u32x4 *>(out + orow * out_cols + c0 + c * 8));
   }
 }
 
