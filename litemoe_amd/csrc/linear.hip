@@ -50,7 +50,14 @@ struct NormIn {
 
 constexpr int kMaxNormTiles = 32;  // K <= 2048
 
-template <int KW, int MB, bool kFragA, bool kNorm = false>
+// kStreamW: the weight tile is read with non-temporal loads. The decode step
+// streams the packed QKV weights this way (lm_linear_splitk, _rmsnorm) and
+// leaves o_proj's (lm_linear_splitk_frag) to the caches: with every other
+// stream-once read of the step non-temporal, o_proj's 4.7 MB per layer then
+// stay in the 256 MB memory-side cache from one step to the next. cfg 3
+// decode step, A/B on one box, three runs each: QKV only 2.784-2.785 ms,
+// o_proj only 2.791-2.793, both 2.810, neither 2.796-2.801.
+template <int KW, int MB, bool kFragA, bool kNorm = false, bool kStreamW = false>
 __global__ void __launch_bounds__(kThreads)
 splitk_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ w, int M, int N,
               int K, float *__restrict__ part, NormIn norm) {
@@ -85,7 +92,9 @@ splitk_kernel(const bf16 *__restrict__ a, int64_t lda, const bf16 *__restrict__ 
   for (int j = 0; j < 2; ++j) {
     const bf16 *wr = w + (int64_t)(n0 + 16 * j + col) * K + k0;
 #pragma unroll
-    for (int t = 0; t < KW; ++t) b[j][t] = load16(wr + t * 32);
+    for (int t = 0; t < KW; ++t)
+      b[j][t] = kStreamW ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wr + t * 32))
+                         : load16(wr + t * 32);
   }
   if constexpr (kNorm) {
     __builtin_amdgcn_sched_barrier(0);
@@ -194,7 +203,7 @@ splitk_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
 
 int row_blocks(int64_t M) { return frag_row_blocks(M); }
 
-template <bool kFragA, bool kNorm = false>
+template <bool kFragA, bool kNorm = false, bool kStreamW = false>
 int launch_splitk(const bf16 *a, int64_t lda, const bf16 *weight, int64_t rows,
                   int64_t out_features, int64_t in_features, int64_t splits, float *partials,
                   hipStream_t s, NormIn norm = NormIn{}) {
@@ -204,7 +213,7 @@ int launch_splitk(const bf16 *a, int64_t lda, const bf16 *weight, int64_t rows,
   const int mb = row_blocks(rows);
 #define LM_SPLITK(KW, MB)                                                                          \
   if (kw == KW && mb == MB) {                                                                      \
-    splitk_kernel<KW, MB, kFragA, kNorm><<<grid, kThreads, 0, s>>>(a, lda, weight, M, N, K, partials, \
+    splitk_kernel<KW, MB, kFragA, kNorm, kStreamW><<<grid, kThreads, 0, s>>>(a, lda, weight, M, N, K, partials, \
                                                                      norm);                       \
     LM_CHECK_LAUNCH();                                                                             \
     return LM_OK;                                                                                  \
@@ -236,8 +245,9 @@ extern "C" int lm_linear_splitk(const void *a, int64_t lda, const void *weight, 
   if (rows == 0) return LM_OK;
   if (!splitk_shape_ok(rows, out_features, in_features, splits)) return LM_EUNSUPPORTED;
   LM_REQUIRE(a && weight && partials);
-  return launch_splitk<false>((const bf16 *)a, lda, (const bf16 *)weight, rows, out_features,
-                              in_features, splits, partials, (hipStream_t)stream);
+  return launch_splitk<false, false, true>((const bf16 *)a, lda, (const bf16 *)weight, rows,
+                                           out_features, in_features, splits, partials,
+                                           (hipStream_t)stream);
 }
 
 extern "C" int lm_linear_splitk_frag(const void *a_frag, const void *weight, int64_t rows,
@@ -262,7 +272,7 @@ extern "C" int lm_linear_splitk_rmsnorm(const void *x, const float *sumsq, const
       in_features / 64 > kMaxNormTiles)
     return LM_EUNSUPPORTED;
   LM_REQUIRE(x && sumsq && norm_weight && weight && partials);
-  return launch_splitk<false, true>((const bf16 *)x, in_features, (const bf16 *)weight, rows,
+  return launch_splitk<false, true, true>((const bf16 *)x, in_features, (const bf16 *)weight, rows,
                                     out_features, in_features, splits, partials,
                                     (hipStream_t)stream,
                                     NormIn{sumsq, (const bf16 *)norm_weight, eps});
