@@ -299,8 +299,13 @@ constexpr int kHeadPhaseBytes = LM_HEAD_PHASE_KB << 10;
 
 __device__ __forceinline__ u32x4 load16(const bf16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
+// Vocabulary tiles per wave. With the head read non-temporal, 2 (385
+// workgroups at the Granite vocabulary, about one and a half waves per SIMD)
+// beats 3 (257 workgroups, one wave per SIMD): the cfg 3 decode step
+// 2.777-2.780 -> 2.768-2.769 ms, 1 tile 2.770 ms (A/B on one box, three runs
+// each). Before the head's loads were non-temporal the three were level.
 template <int MB>
-constexpr int head_tiles_per_wave() { return MB <= 4 ? 3 : 2; }
+constexpr int head_tiles_per_wave() { return 2; }
 
 // k-steps per phase: the largest divisor of KS whose phase fits the LDS
 // budget (a k-step of z is MB*16 rows x 64 bytes).
