@@ -456,6 +456,41 @@ def test_flash_decode_matches_oracle(b, hq, hkv, cap, low, high, splits):
     assert rel_l2(got[rows], exp) < 5e-3
 
 
+@pytest.mark.parametrize("pattern", ["ramp", "sawtooth", "wide", "falling"])
+@pytest.mark.parametrize("splits", [None, 3])
+@torch.inference_mode()
+def test_flash_decode_score_drift_matches_oracle(pattern, splits):
+    """Scores that move the running maximum many times, by steps below and
+    above the kernel's slack of 8 (log2 units) before it rescales: a ramp of
+    0.06 per key up to ~60, a sawtooth of +5 / +11 jumps, a spread of std 20,
+    and a falling ramp (the maximum at the first key)."""
+    b, hq, hkv, cap = 6, 24, 8, 1024
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(b, hq, 64, generator=g)
+    j = torch.arange(cap, dtype=torch.float32)
+    if pattern == "ramp":
+        t = 0.06 * j - 10
+    elif pattern == "sawtooth":
+        t = torch.where((j // 16) % 2 == 0, 5.0, 11.0) * (j // 16 % 5) + 0.01 * j
+    elif pattern == "wide":
+        t = 20 * torch.randn(cap, generator=g)
+    else:
+        t = 30 - 0.05 * j
+    # k of kv head h lies along q of its group's first q head: scale * q.k = t (natural log units)
+    lead = q[:, ::hq // hkv]  # [b, hkv, 64]
+    kc = t[None, None, :, None] * lead[:, :, None, :] / (0.125 * lead.square().sum(-1))[:, :, None, None]
+    kc = (kc + 0.05 * torch.randn(b, hkv, cap, 64, generator=g)).to(torch.bfloat16)
+    q = q.to(torch.bfloat16)
+    vc = torch.randn(b, hkv, cap, 64, generator=g).to(torch.bfloat16)
+    used = torch.tensor([1024, 1000, 777, 300, 129, 17], dtype=torch.int32)
+    fd = flash_decode.FlashDecode(b, hkv, hq // hkv, cap, DEV, maximum=cap, num_splits=splits)
+    got = fd(q.to(DEV)[:, :, None], kc.to(DEV), vc.to(DEV), None, None, 0.125, used=used.to(DEV))[:, :, 0].cpu()
+    exp = ops.decode_attention(q, kc, vc, used, 0.125)
+    assert torch.isfinite(got.float()).all()
+    torch.testing.assert_close(got, exp, atol=.004, rtol=.03)
+    assert rel_l2(got, exp) < 5e-3
+
+
 @torch.inference_mode()
 def test_flash_decode_lengths_active_and_empty_rows():
     b, hq, hkv, cap = 4, 6, 2, 64
