@@ -40,9 +40,11 @@ def test_workspace_queries():
     assert _lib.size_query("lm_flash_decode_workspace_size", 64, 24, 64, 1) == 0
     n = 64 * 24 * 5
     assert _lib.size_query("lm_flash_decode_workspace_size", 64, 24, 64, 5) == n * 256 + 2 * n * 4
-    # fused head: one 8-byte argmax word per row and slice of 12 vocabulary tiles (8 above 64 rows)
-    assert _lib.size_query("lm_head_greedy_workspace_size", 64, 49155, 1536) == 64 * 257 * 8
+    # fused head: one 8-byte argmax word per row and slice of 8 vocabulary tiles (4 waves x 2 tiles);
+    # 49155 rows are 3073 tiles of 16, i.e. 385 slices
+    assert _lib.size_query("lm_head_greedy_workspace_size", 64, 49155, 1536) == 64 * 385 * 8
     assert _lib.size_query("lm_head_greedy_workspace_size", 128, 49155, 1536) == 128 * 385 * 8
+    assert _lib.size_query("lm_head_greedy_workspace_size", 16, 1000, 512) == 16 * 8 * 8
 
 
 # Non-null dummy pointers: every case returns before any launch, so nothing
