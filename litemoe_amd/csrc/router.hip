@@ -610,8 +610,10 @@ __device__ __forceinline__ void batch_norm_row(bf16 *__restrict__ x, float alpha
   }
 }
 
+// Occupancy target: four waves per SIMD up to hidden 1536 and 48 experts;
+// the 49-64 expert tiles need more registers (three waves), wider rows two.
 template <int NVL, int NT, bool kNorm, bool kAdd>
-__global__ void __launch_bounds__(kBatchThreads, NVL <= 3 ? 4 : 2)
+__global__ void __launch_bounds__(kBatchThreads, NVL <= 3 ? (NT <= 3 ? 4 : 3) : 2)
 batched_router_kernel(bf16 *__restrict__ x, const bf16 *__restrict__ a, float alpha,
                       const bf16 *__restrict__ nw, float eps, bf16 *__restrict__ z,
                       const bf16 *__restrict__ wr, int experts, int topk, int renormalize,

@@ -643,7 +643,7 @@ def per_token_logits(z, wr, k, chunk=256):
 @pytest.mark.parametrize("m,h,e,k,with_residual", [(4103, 1536, 40, 8, True), (4096, 1536, 40, 8, False),
                                                    (4111, 1024, 32, 4, True), (4100, 4096, 64, 8, True),
                                                    (4096, 3072, 60, 6, True), (4104, 512, 20, 2, True),
-                                                   (4097, 2048, 48, 8, True)])
+                                                   (4097, 2048, 48, 8, True), (4100, 1536, 64, 8, True)])
 @torch.inference_mode()
 def test_batched_add_rmsnorm_route(m, h, e, k, with_residual):
     """Prefill-sized calls take the batched MFMA router (16 tokens per wave,
